@@ -1,0 +1,263 @@
+"""ctypes binding of include/bonsai_attn.h (the C ABI of libbonsai_attn.so).
+
+This is the binding a Python caller (tests, benchmark) uses; the Rust runtime binds the same symbols through
+an `extern "C"` block. Device memory and streams come from the caller: here torch tensors on a ROCm device
+supply raw pointers (torch is plumbing only; the library itself never sees a torch type).
+
+The product path has no fallback: if the library is missing, `load()` raises.
+"""
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libbonsai_attn.so")
+
+D = 256
+VERIFY_MAX = 16
+
+BN_OK, BN_EINVAL, BN_ENOWS, BN_ELAUNCH, BN_EDEVICE = 0, 1, 2, 3, 4
+BN_Q_F16 = 1
+KIND_FORWARD, KIND_DECODE, KIND_VERIFY, KIND_PREFILL, KIND_APPEND = 0, 1, 2, 3, 4
+
+# every symbol include/bonsai_attn.h declares
+EXPORTS = (
+    "bn_ctx_create", "bn_ctx_destroy", "bn_status_str", "bn_ctx_last_error", "bn_abi_version",
+    "bn_attn_workspace_size", "bn_ragged_workspace_size", "bn_attn_check", "bn_ragged_check",
+    "bn_workspace_clear", "bn_attn_forward", "bn_attn_decode", "bn_attn_verify", "bn_attn_prefill",
+    "bn_attn_append", "bn_attn_decode_ragged",
+)
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("T", ctypes.c_uint32), ("off", ctypes.c_uint32), ("H", ctypes.c_uint32), ("KV", ctypes.c_uint32),
+        ("cap", ctypes.c_uint32), ("flags", ctypes.c_uint32),
+        ("q", ctypes.c_void_p), ("q_ts", ctypes.c_int64), ("q_hs", ctypes.c_int64),
+        ("k_new", ctypes.c_void_p), ("v_new", ctypes.c_void_p),
+        ("kc", ctypes.c_void_p), ("vc", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p), ("g_ts", ctypes.c_int64), ("g_hs", ctypes.c_int64),
+        ("out", ctypes.c_void_p), ("o_ts", ctypes.c_int64), ("o_hs", ctypes.c_int64),
+        ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t),
+    ]
+
+
+class RaggedArgs(ctypes.Structure):
+    _fields_ = [
+        ("nseq", ctypes.c_uint32), ("H", ctypes.c_uint32), ("KV", ctypes.c_uint32), ("max_len", ctypes.c_uint32),
+        ("q", ctypes.c_void_p), ("q_ss", ctypes.c_int64), ("q_hs", ctypes.c_int64),
+        ("k_new", ctypes.c_void_p), ("v_new", ctypes.c_void_p),
+        ("kc", ctypes.c_void_p), ("vc", ctypes.c_void_p),
+        ("kv_off", ctypes.c_void_p), ("kv_len", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p), ("g_ss", ctypes.c_int64), ("g_hs", ctypes.c_int64),
+        ("out", ctypes.c_void_p), ("o_ss", ctypes.c_int64), ("o_hs", ctypes.c_int64),
+        ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t),
+    ]
+
+
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Loads the HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with glimpse-language_amd/build.py")
+    lib = ctypes.CDLL(path)
+    P = ctypes.c_void_p
+    lib.bn_ctx_create.argtypes = [ctypes.c_int, ctypes.POINTER(P)]
+    lib.bn_ctx_create.restype = ctypes.c_int
+    lib.bn_ctx_destroy.argtypes = [P]
+    lib.bn_ctx_destroy.restype = None
+    lib.bn_status_str.argtypes = [ctypes.c_int]
+    lib.bn_status_str.restype = ctypes.c_char_p
+    lib.bn_ctx_last_error.argtypes = [P]
+    lib.bn_ctx_last_error.restype = ctypes.c_char_p
+    lib.bn_abi_version.argtypes = []
+    lib.bn_abi_version.restype = ctypes.c_int
+    lib.bn_attn_workspace_size.argtypes = [ctypes.POINTER(AttnArgs)]
+    lib.bn_attn_workspace_size.restype = ctypes.c_size_t
+    lib.bn_ragged_workspace_size.argtypes = [ctypes.POINTER(RaggedArgs)]
+    lib.bn_ragged_workspace_size.restype = ctypes.c_size_t
+    lib.bn_attn_check.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_int]
+    lib.bn_attn_check.restype = ctypes.c_int
+    lib.bn_ragged_check.argtypes = [ctypes.POINTER(RaggedArgs)]
+    lib.bn_ragged_check.restype = ctypes.c_int
+    lib.bn_workspace_clear.argtypes = [P, P, P, ctypes.c_size_t]
+    lib.bn_workspace_clear.restype = ctypes.c_int
+    for name in ("bn_attn_forward", "bn_attn_decode", "bn_attn_verify", "bn_attn_prefill", "bn_attn_append"):
+        f = getattr(lib, name)
+        f.argtypes = [P, P, ctypes.POINTER(AttnArgs)]
+        f.restype = ctypes.c_int
+    lib.bn_attn_decode_ragged.argtypes = [P, P, ctypes.POINTER(RaggedArgs)]
+    lib.bn_attn_decode_ragged.restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+class BonsaiAttnError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"{msg} (status {status})")
+        self.status = status
+
+
+def last_check_error():
+    return load().bn_ctx_last_error(None).decode()
+
+
+class Context:
+    """bn_ctx on one device. Calls are ordered on the given stream (default: torch's current stream)."""
+
+    def __init__(self, device=0):
+        lib = load()
+        h = ctypes.c_void_p()
+        st = lib.bn_ctx_create(device, ctypes.byref(h))
+        if st != BN_OK:
+            raise BonsaiAttnError(st, f"bn_ctx_create({device}) failed: {lib.bn_status_str(st).decode()}")
+        self.h = h
+        self.lib = lib
+        self.device = device
+
+    def close(self):
+        if self.h:
+            self.lib.bn_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def error(self):
+        return self.lib.bn_ctx_last_error(self.h).decode()
+
+    def _stream(self, stream):
+        if stream is not None:
+            return ctypes.c_void_p(int(stream))
+        import torch
+        return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def _check(self, st, what):
+        if st != BN_OK:
+            raise BonsaiAttnError(st, f"{what}: {self.error()}")
+
+    def call(self, name, args, stream=None):
+        f = getattr(self.lib, name)
+        st = f(self.h, self._stream(stream), ctypes.byref(args))
+        self._check(st, name)
+
+    def workspace_clear(self, ws_ptr, nbytes, stream=None):
+        st = self.lib.bn_workspace_clear(self.h, self._stream(stream), ctypes.c_void_p(ws_ptr), nbytes)
+        self._check(st, "bn_workspace_clear")
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def attn_args(T, off, H, KV, cap, q, kc, vc, out, k_new=None, v_new=None, gate=None, ws=None, flags=0,
+              q_strides=None, g_strides=None, o_strides=None):
+    """bn_attn_args from tensors. q [T][H][256] (or explicit strides), gate/out likewise; kc/vc fp16 caches
+    viewed as int16/float16 tensors; ws a byte tensor or None."""
+    a = AttnArgs()
+    a.T, a.off, a.H, a.KV, a.cap, a.flags = T, off, H, KV, cap, flags
+    a.q = _ptr(q)
+    a.q_ts, a.q_hs = q_strides if q_strides else (H * D, D)
+    a.k_new, a.v_new = _ptr(k_new), _ptr(v_new)
+    a.kc, a.vc = _ptr(kc), _ptr(vc)
+    a.gate = _ptr(gate)
+    a.g_ts, a.g_hs = g_strides if g_strides else (H * D, D)
+    a.out = _ptr(out)
+    a.o_ts, a.o_hs = o_strides if o_strides else (H * D, D)
+    a.ws = _ptr(ws)
+    a.ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    return a
+
+
+def ragged_args(nseq, H, KV, max_len, q, kc, vc, kv_off, kv_len, out, k_new=None, v_new=None, gate=None,
+                ws=None):
+    a = RaggedArgs()
+    a.nseq, a.H, a.KV, a.max_len = nseq, H, KV, max_len
+    a.q, a.q_ss, a.q_hs = _ptr(q), H * D, D
+    a.k_new, a.v_new = _ptr(k_new), _ptr(v_new)
+    a.kc, a.vc = _ptr(kc), _ptr(vc)
+    a.kv_off, a.kv_len = _ptr(kv_off), _ptr(kv_len)
+    a.gate, a.g_ss, a.g_hs = _ptr(gate), H * D, D
+    a.out, a.o_ss, a.o_hs = _ptr(out), H * D, D
+    a.ws = _ptr(ws)
+    a.ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    return a
+
+
+def workspace_size(args):
+    lib = load()
+    if isinstance(args, RaggedArgs):
+        return lib.bn_ragged_workspace_size(ctypes.byref(args))
+    return lib.bn_attn_workspace_size(ctypes.byref(args))
+
+
+def check(args, kind=KIND_FORWARD):
+    lib = load()
+    if isinstance(args, RaggedArgs):
+        return lib.bn_ragged_check(ctypes.byref(args))
+    return lib.bn_attn_check(ctypes.byref(args), kind)
+
+
+class Workspace:
+    """A caller-owned, zero-initialised device workspace that grows on demand (torch uint8 tensor)."""
+
+    def __init__(self, ctx, device="cuda"):
+        self.ctx = ctx
+        self.device = device
+        self.buf = None
+
+    def get(self, nbytes):
+        import torch
+        if nbytes == 0:
+            return None
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self.ctx.workspace_clear(self.buf.data_ptr(), self.buf.numel())
+        return self.buf
+
+
+_KIND_FN = {KIND_FORWARD: "bn_attn_forward", KIND_DECODE: "bn_attn_decode", KIND_VERIFY: "bn_attn_verify",
+            KIND_PREFILL: "bn_attn_prefill", KIND_APPEND: "bn_attn_append"}
+
+
+def attention(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=None, kind=KIND_FORWARD,
+              stream=None, q_strides=None, g_strides=None):
+    """One attention-layer call: append k_new/v_new at [off, off+T), attend causally, gate.
+
+    q: [T, H, 256] fp32; kc/vc: [cap, KV, 256] fp16 (torch.float16 or int16 view); out: [T, H, 256] fp32.
+    """
+    import torch
+    T, H = q.shape[0], q.shape[1]
+    cap, KV = kc.shape[0], kc.shape[1]
+    if out is None:
+        out = torch.empty((T, H, D), dtype=torch.float32, device=q.device)
+    a = attn_args(T, off, H, KV, cap, q, kc, vc, out, k_new, v_new, gate, None, 0, q_strides, g_strides)
+    need = workspace_size(a)
+    buf = ws.get(need) if ws is not None else None
+    a.ws = _ptr(buf)
+    a.ws_bytes = 0 if buf is None else buf.numel()
+    ctx.call(_KIND_FN[kind], a, stream)
+    return out
+
+
+def decode_ragged(ctx, ws, q, kc, vc, kv_off, kv_len, max_len, out=None, k_new=None, v_new=None, gate=None,
+                  stream=None):
+    import torch
+    nseq, H = q.shape[0], q.shape[1]
+    KV = kc.shape[1]
+    if out is None:
+        out = torch.empty((nseq, H, D), dtype=torch.float32, device=q.device)
+    a = ragged_args(nseq, H, KV, max_len, q, kc, vc, kv_off, kv_len, out, k_new, v_new, gate)
+    need = workspace_size(a)
+    buf = ws.get(need) if ws is not None else None
+    a.ws = _ptr(buf)
+    a.ws_bytes = 0 if buf is None else buf.numel()
+    ctx.call("bn_attn_decode_ragged", a, stream)
+    return out

@@ -1,0 +1,325 @@
+// C ABI of the gfx950 attention path (include/bonsai_attn.h): argument checks, split policy, workspace
+// layout and kernel launches. Host logic only; the kernels live in the bn_*.h headers.
+#include "bonsai_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "bn_decode.h"
+#include "bn_util_kernels.h"
+
+struct bn_ctx {
+    int device;
+    int cus;
+    char err[256];
+};
+
+namespace {
+
+thread_local char g_check_err[256];
+
+constexpr int kVerifyMax = 16;     // verify rows handled by the verify kernel (model.rs VMAX = 16)
+constexpr int64_t kMaxRows = 1 << 24;  // positions addressable by one call (int32 key indices)
+
+bn_status set_err(char* buf, bn_status s, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, 256, fmt, ap);
+    va_end(ap);
+    return s;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+int64_t ceil_div(int64_t x, int64_t m) { return (x + m - 1) / m; }
+
+// Keys per split for single-token decodes: about 4096 one-wave blocks over the whole launch, at least
+// 64 keys per split and at most 64 splits per (sequence, kv head). Depends only on the shapes, so a
+// given shape always gets the same split structure (and the same bits).
+int64_t decode_chunk(int64_t max_len, int64_t pairs) {
+    int64_t target = 4096 / (pairs > 0 ? pairs : 1);
+    if (target < 1) target = 1;
+    int64_t chunk = round_up(ceil_div(max_len, target), 16);
+    if (chunk < 64) chunk = 64;
+    int64_t cap64 = round_up(ceil_div(max_len, 64), 16);
+    if (chunk < cap64) chunk = cap64;
+    return chunk;
+}
+
+struct DecodePlan {
+    int64_t nseq, KV, max_len, chunk, max_splits;
+    size_t cnt_bytes, part_bytes;
+    size_t total() const { return max_splits > 1 ? cnt_bytes + part_bytes : 0; }
+};
+
+DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len) {
+    DecodePlan p;
+    p.nseq = nseq;
+    p.KV = KV;
+    p.max_len = max_len;
+    p.chunk = decode_chunk(max_len, nseq * KV);
+    p.max_splits = ceil_div(max_len, p.chunk);
+    p.cnt_bytes = (size_t)round_up(nseq * KV * 4, 256);
+    p.part_bytes = (size_t)(nseq * KV * p.max_splits) * bn::DEC_PART * sizeof(float);
+    return p;
+}
+
+// Rows handled per launch by the row-wise path (verify / prefill through the decode kernel).
+DecodePlan plan_rows(const bn_attn_args* a) { return plan_decode(a->T, a->KV, (int64_t)a->off + a->T); }
+
+bn_status check_attn(const bn_attn_args* a, int kind, char* why) {
+    if (!a) return set_err(why, BN_EINVAL, "args is NULL");
+    if (kind < 0 || kind > 4) return set_err(why, BN_EINVAL, "unknown kind %d", kind);
+    if (a->KV < 1 || a->H != 4 * a->KV)
+        return set_err(why, BN_EINVAL, "need H == 4*KV >= 4 (H=%u KV=%u)", a->H, a->KV);
+    if (a->T < 1) return set_err(why, BN_EINVAL, "T must be >= 1");
+    if (kind == 1 && a->T != 1) return set_err(why, BN_EINVAL, "decode takes T == 1 (T=%u)", a->T);
+    if (kind == 2 && a->T > (uint32_t)kVerifyMax)
+        return set_err(why, BN_EINVAL, "verify takes T <= %d (T=%u)", kVerifyMax, a->T);
+    if ((uint64_t)a->off + a->T > a->cap)
+        return set_err(why, BN_EINVAL, "off + T = %llu exceeds cap = %u", (unsigned long long)a->off + a->T, a->cap);
+    if ((int64_t)a->off + a->T > kMaxRows) return set_err(why, BN_EINVAL, "off + T beyond %lld", (long long)kMaxRows);
+    if (a->flags & ~BN_Q_F16) return set_err(why, BN_EINVAL, "unknown flags 0x%x", a->flags);
+    if (a->flags & BN_Q_F16) return set_err(why, BN_EINVAL, "BN_Q_F16 is not supported by this build");
+    if (!a->kc || !a->vc) return set_err(why, BN_EINVAL, "kc and vc are required");
+    if (!aligned16(a->kc) || !aligned16(a->vc)) return set_err(why, BN_EINVAL, "kc/vc must be 16-byte aligned");
+    if ((a->k_new == nullptr) != (a->v_new == nullptr))
+        return set_err(why, BN_EINVAL, "k_new and v_new are given together or not at all");
+    if (a->k_new && (!aligned16(a->k_new) || !aligned16(a->v_new)))
+        return set_err(why, BN_EINVAL, "k_new/v_new must be 16-byte aligned");
+    if (kind == 4) {
+        if (!a->k_new) return set_err(why, BN_EINVAL, "append needs k_new and v_new");
+        return BN_OK;
+    }
+    if (!a->q || !a->out) return set_err(why, BN_EINVAL, "q and out are required");
+    if (!aligned16(a->out) || (a->o_ts & 3) || (a->o_hs & 3) || a->o_ts < 0 || a->o_hs < 0)
+        return set_err(why, BN_EINVAL, "out must be 16-byte aligned with strides that are multiples of 4 floats");
+    if (a->q_ts < 0 || a->q_hs < 0 || ((uintptr_t)a->q & 3))
+        return set_err(why, BN_EINVAL, "bad q pointer or strides");
+    if (a->gate && (a->g_ts < 0 || a->g_hs < 0 || ((uintptr_t)a->gate & 3)))
+        return set_err(why, BN_EINVAL, "bad gate pointer or strides");
+    size_t need = bn_attn_workspace_size(a);
+    if (need && (!a->ws || a->ws_bytes < need || !aligned16(a->ws)))
+        return set_err(why, BN_ENOWS, "workspace needs %zu bytes (16-byte aligned), got %zu", need, a->ws_bytes);
+    return BN_OK;
+}
+
+bn_status check_ragged(const bn_ragged_args* a, char* why) {
+    if (!a) return set_err(why, BN_EINVAL, "args is NULL");
+    if (a->nseq < 1 || a->nseq > 65535) return set_err(why, BN_EINVAL, "nseq must be in 1..65535");
+    if (a->KV < 1 || a->H != 4 * a->KV)
+        return set_err(why, BN_EINVAL, "need H == 4*KV >= 4 (H=%u KV=%u)", a->H, a->KV);
+    if (a->max_len < 1 || a->max_len > kMaxRows) return set_err(why, BN_EINVAL, "max_len out of range");
+    if (!a->q || !a->out || !a->kc || !a->vc || !a->kv_off || !a->kv_len)
+        return set_err(why, BN_EINVAL, "q, out, kc, vc, kv_off and kv_len are required");
+    if (!aligned16(a->kc) || !aligned16(a->vc)) return set_err(why, BN_EINVAL, "kc/vc must be 16-byte aligned");
+    if ((a->k_new == nullptr) != (a->v_new == nullptr))
+        return set_err(why, BN_EINVAL, "k_new and v_new are given together or not at all");
+    if (a->k_new && (!aligned16(a->k_new) || !aligned16(a->v_new)))
+        return set_err(why, BN_EINVAL, "k_new/v_new must be 16-byte aligned");
+    if (!aligned16(a->out) || (a->o_ss & 3) || (a->o_hs & 3) || a->o_ss < 0 || a->o_hs < 0)
+        return set_err(why, BN_EINVAL, "out must be 16-byte aligned with strides that are multiples of 4 floats");
+    if (a->q_ss < 0 || a->q_hs < 0 || ((uintptr_t)a->q & 3)) return set_err(why, BN_EINVAL, "bad q pointer or strides");
+    if (a->gate && (a->g_ss < 0 || a->g_hs < 0 || ((uintptr_t)a->gate & 3)))
+        return set_err(why, BN_EINVAL, "bad gate pointer or strides");
+    size_t need = bn_ragged_workspace_size(a);
+    if (need && (!a->ws || a->ws_bytes < need || !aligned16(a->ws)))
+        return set_err(why, BN_ENOWS, "workspace needs %zu bytes (16-byte aligned), got %zu", need, a->ws_bytes);
+    return BN_OK;
+}
+
+bn_status launched(bn_ctx* ctx, const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_err(ctx->err, BN_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return BN_OK;
+}
+
+bn_status launch_append(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    const int64_t row = (int64_t)a->KV * bn::D;
+    const int64_t n8 = (int64_t)a->T * row / 8;
+    int64_t blocks = ceil_div(n8, 256);
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(bn::append_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a->k_new, a->v_new,
+                       a->kc + (int64_t)a->off * row, a->vc + (int64_t)a->off * row, n8);
+    return launched(ctx, "append_kernel");
+}
+
+bn_status launch_decode(bn_ctx* ctx, hipStream_t st, const bn::DecodeArgs& d, const DecodePlan& p) {
+    dim3 grid((unsigned)p.max_splits, (unsigned)p.KV, (unsigned)p.nseq);
+    hipLaunchKernelGGL(bn::decode_kernel, grid, dim3(64), 0, st, d);
+    return launched(ctx, "decode_kernel");
+}
+
+void bind_workspace(bn::DecodeArgs& d, const DecodePlan& p, void* ws) {
+    d.chunk = (int)p.chunk;
+    d.max_splits = (int)p.max_splits;
+    d.max_len = (int)p.max_len;
+    d.cnt = p.max_splits > 1 ? static_cast<uint32_t*>(ws) : nullptr;
+    d.part = p.max_splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.cnt_bytes) : nullptr;
+}
+
+// T query rows of one sequence as T single-row decodes over the shared cache (row t sees off+t+1 keys).
+bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    if (a->T > 65535) return set_err(ctx->err, BN_EINVAL, "T = %u rows exceeds the row-wise launch (65535)", a->T);
+    const bool fused_append = a->T == 1;
+    if (a->k_new && !fused_append) {
+        bn_status s = launch_append(ctx, st, a);
+        if (s) return s;
+    }
+    DecodePlan p = plan_rows(a);
+    bn::DecodeArgs d{};
+    d.q = static_cast<const float*>(a->q);
+    d.q_ss = a->q_ts;
+    d.q_hs = a->q_hs;
+    d.k_new = fused_append ? a->k_new : nullptr;
+    d.v_new = fused_append ? a->v_new : nullptr;
+    d.kn_ss = (int64_t)a->KV * bn::D;
+    d.kc = a->kc;
+    d.vc = a->vc;
+    d.row0 = 0;
+    d.row_step = 0;
+    d.len0 = (int32_t)a->off + 1;
+    d.len_step = 1;
+    d.gate = a->gate;
+    d.g_ss = a->g_ts;
+    d.g_hs = a->g_hs;
+    d.out = a->out;
+    d.o_ss = a->o_ts;
+    d.o_hs = a->o_hs;
+    d.KV = (int)a->KV;
+    bind_workspace(d, p, a->ws);
+    return launch_decode(ctx, st, d, p);
+}
+
+}  // namespace
+
+extern "C" {
+
+int bn_abi_version(void) { return BN_ABI_VERSION; }
+
+const char* bn_status_str(bn_status s) {
+    switch (s) {
+        case BN_OK: return "ok";
+        case BN_EINVAL: return "invalid argument";
+        case BN_ENOWS: return "workspace too small";
+        case BN_ELAUNCH: return "kernel launch failed";
+        case BN_EDEVICE: return "device error";
+    }
+    return "unknown status";
+}
+
+bn_status bn_ctx_create(int device, bn_ctx** out) {
+    if (!out) return BN_EINVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return BN_EDEVICE;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return BN_EDEVICE;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return BN_EDEVICE;
+    bn_ctx* c = new (std::nothrow) bn_ctx;
+    if (!c) return BN_EDEVICE;
+    c->device = device;
+    c->cus = prop.multiProcessorCount;
+    c->err[0] = 0;
+    *out = c;
+    return BN_OK;
+}
+
+void bn_ctx_destroy(bn_ctx* ctx) { delete ctx; }
+
+const char* bn_ctx_last_error(const bn_ctx* ctx) { return ctx ? ctx->err : g_check_err; }
+
+size_t bn_attn_workspace_size(const bn_attn_args* a) {
+    if (!a || a->KV < 1 || a->T < 1) return 0;
+    return plan_rows(a).total();
+}
+
+size_t bn_ragged_workspace_size(const bn_ragged_args* a) {
+    if (!a || a->KV < 1 || a->nseq < 1 || a->max_len < 1) return 0;
+    return plan_decode(a->nseq, a->KV, a->max_len).total();
+}
+
+bn_status bn_attn_check(const bn_attn_args* a, int kind) { return check_attn(a, kind, g_check_err); }
+
+bn_status bn_ragged_check(const bn_ragged_args* a) { return check_ragged(a, g_check_err); }
+
+bn_status bn_workspace_clear(bn_ctx* ctx, bn_stream stream, void* ws, size_t bytes) {
+    if (!ctx) return BN_EINVAL;
+    if (!bytes) return BN_OK;
+    if (!ws || !aligned16(ws)) return set_err(ctx->err, BN_EINVAL, "workspace must be 16-byte aligned");
+    int64_t n16 = (int64_t)(bytes / 16);
+    int ntail = (int)(bytes % 16);
+    int64_t blocks = ceil_div(n16 > 0 ? n16 : 1, 256);
+    if (blocks > 2048) blocks = 2048;
+    hipLaunchKernelGGL(bn::fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       static_cast<bn::u4*>(ws), n16, static_cast<uint8_t*>(ws) + n16 * 16, ntail);
+    return launched(ctx, "fill_zero_kernel");
+}
+
+bn_status bn_attn_append(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_attn(a, 4, ctx->err);
+    if (s) return s;
+    return launch_append(ctx, (hipStream_t)stream, a);
+}
+
+bn_status bn_attn_decode(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_attn(a, 1, ctx->err);
+    if (s) return s;
+    return run_rows(ctx, (hipStream_t)stream, a);
+}
+
+bn_status bn_attn_verify(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_attn(a, 2, ctx->err);
+    if (s) return s;
+    return run_rows(ctx, (hipStream_t)stream, a);
+}
+
+bn_status bn_attn_prefill(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_attn(a, 3, ctx->err);
+    if (s) return s;
+    return run_rows(ctx, (hipStream_t)stream, a);
+}
+
+bn_status bn_attn_forward(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_attn(a, 0, ctx->err);
+    if (s) return s;
+    return run_rows(ctx, (hipStream_t)stream, a);
+}
+
+bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_ragged(a, ctx->err);
+    if (s) return s;
+    DecodePlan p = plan_decode(a->nseq, a->KV, a->max_len);
+    bn::DecodeArgs d{};
+    d.q = a->q;
+    d.q_ss = a->q_ss;
+    d.q_hs = a->q_hs;
+    d.k_new = a->k_new;
+    d.v_new = a->v_new;
+    d.kn_ss = (int64_t)a->KV * bn::D;
+    d.kc = a->kc;
+    d.vc = a->vc;
+    d.kv_off = a->kv_off;
+    d.kv_len = a->kv_len;
+    d.gate = a->gate;
+    d.g_ss = a->g_ss;
+    d.g_hs = a->g_hs;
+    d.out = a->out;
+    d.o_ss = a->o_ss;
+    d.o_hs = a->o_hs;
+    d.KV = (int)a->KV;
+    bind_workspace(d, p, a->ws);
+    return launch_decode(ctx, (hipStream_t)stream, d, p);
+}
+
+}  // extern "C"

@@ -1,0 +1,291 @@
+// Split-KV decode attention (one query token per sequence) over an fp16 KV cache.
+//
+// Semantics follow attn_split.comp:9-58 + attn_combine.comp:6-21 + gate_rotate.comp:19-22 of the reference
+// (query row of head h attends to cache rows [0, L) of kv head h/4, softmax(q.k / 16), gate a*sigmoid(z));
+// the decomposition is this kernel's own:
+//   grid (split, kv head, sequence) x one wave. A split covers `chunk` consecutive keys of one kv head and
+//   serves the 4 query heads that share it, so every K/V byte is read once.
+//   QK^T: v_mfma_f32_16x16x32_f16 computes S^T = K Q^T over 16-key tiles. The A operand is the K tile read
+//   straight from HBM in MFMA layout (lane: key l%16, 8 dims per k-step); the B operand holds the 4 heads'
+//   query rows as an fp16 hi/lo pair (columns h and h+4, repeated in 8..15), so hi + lo carries the fp32
+//   query and the scores are fp32-accurate at no extra MFMA cost.
+//   Softmax: online, in the log2 domain (q pre-scaled by log2 e), fp32.
+//   PV: fp32 FMAs on the VALU; each lane owns 8 dims of every other key and the 4 heads.
+//   Combine: each split writes (m, l, acc[256]) per head to the workspace; the last split to finish
+//   (device-scope counter) merges all splits in split order, applies the gate and writes the output, then
+//   re-arms the counter. The merge order is fixed, so results do not depend on scheduling.
+//   Append: when k_new/v_new are given, the new row (last key of the sequence) is taken from them, rounded
+//   to fp16, used for the score and the PV product, and stored into the cache by the same split.
+#pragma once
+#include "bn_device.h"
+
+namespace bn {
+
+constexpr int DEC_PART = 8 + 4 * D;  // per (sequence, kv head, split): m[4], l[4], acc[4][256] (floats)
+
+struct DecodeArgs {
+    const float* q;      // element seq*q_ss + head*q_hs + d
+    int64_t q_ss, q_hs;
+    const float* k_new;  // element seq*kn_ss + kh*256 + d, or null
+    const float* v_new;
+    int64_t kn_ss;
+    uint16_t* kc;        // fp16 rows [row][KV][256]
+    uint16_t* vc;
+    const int64_t* kv_off;  // device: first cache row of each sequence (null: row0 + seq*row_step)
+    const int32_t* kv_len;  // device: keys of each sequence (null: len0 + seq*len_step)
+    int64_t row0, row_step;
+    int32_t len0, len_step;
+    const float* gate;   // element seq*g_ss + head*g_hs + d, or null
+    int64_t g_ss, g_hs;
+    float* out;          // element seq*o_ss + head*o_hs + d
+    int64_t o_ss, o_hs;
+    float* part;         // [nseq][KV][max_splits][DEC_PART]
+    uint32_t* cnt;       // [nseq][KV], zero between calls
+    int KV, chunk, max_splits, max_len;
+};
+
+__global__ __launch_bounds__(64) void decode_kernel(DecodeArgs a) {
+    __shared__ f4 p_lds[16];   // p[key in tile][head]
+    __shared__ f4 al_lds;      // per-head rescale of the running accumulators
+    __shared__ f4 ml_lds[2];   // final m, l per head
+    __shared__ int last_lds;
+
+    const int s = blockIdx.x, kh = blockIdx.y, seq = blockIdx.z;
+    const int lane = threadIdx.x;
+    // keys of this sequence; device-supplied lengths are clamped to the launch bound
+    const int L = min(a.kv_len ? a.kv_len[seq] : a.len0 + seq * a.len_step, a.max_len);
+    const int64_t row0 = a.kv_off ? a.kv_off[seq] : a.row0 + (int64_t)seq * a.row_step;
+    const int ns = L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
+    if (s >= ns) return;
+    const int j0 = s * a.chunk;
+    const int j1 = min(L, j0 + a.chunk);
+    const bool append = a.k_new != nullptr;
+    const bool has_new = append && j1 == L;   // this split owns the appended row L-1
+    const int jend = has_new ? L - 1 : j1;    // keys [j0, jend) come from the cache
+    const int64_t kvd = (int64_t)a.KV * D;
+    const uint16_t* kb = a.kc + (row0 * a.KV + kh) * D;
+    const uint16_t* vb = a.vc + (row0 * a.KV + kh) * D;
+
+    const int c = lane & 15, g = lane >> 4;       // MFMA column / k-group of this lane
+    const int pvr = lane >> 5, pvd = (lane & 31) * 8;  // PV layout: key parity, first dim
+
+    // B operand: Q^T, column c = head (c&3), hi part for (c&4)==0 else lo part, k-step ks covers
+    // dims ks*32 + g*8 .. +7.
+    h8 qb[8];
+    {
+        const float* qr = a.q + seq * a.q_ss + (int64_t)(kh * 4 + (c & 3)) * a.q_hs + g * 8;
+        const bool lo = (c & 4) != 0;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float x = qr[ks * 32 + e] * LOG2E;
+                _Float16 hi = (_Float16)x;
+                qb[ks][e] = lo ? (_Float16)(x - (float)hi) : hi;
+            }
+        }
+    }
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    float acc[4][8];
+#pragma unroll
+    for (int h = 0; h < 4; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
+
+    auto tile = [&](const h8* kt, const h8* vt, int jt, int jlim) {
+        f4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) sacc = mfma16(kt[ks], qb[ks], sacc);
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float v = (sacc[r] + __shfl_xor(sacc[r], 4)) * QK_SCALE;
+            sc[r] = (jt + 4 * g + r < jlim) ? v : -INFINITY;
+        }
+        float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        tm = fmaxf(tm, __shfl_xor(tm, 16));
+        tm = fmaxf(tm, __shfl_xor(tm, 32));
+        const float m_new = fmaxf(m_run, tm);
+        const float alpha = exp2f(m_run - m_new);
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) p[r] = exp2f(sc[r] - m_new);
+        l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+        m_run = m_new;
+        if (c < 4) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) p_lds[4 * g + r][c] = p[r];
+            if (g == 0) al_lds[c] = alpha;
+        }
+        __syncthreads();
+        const f4 al = al_lds;
+#pragma unroll
+        for (int h = 0; h < 4; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[h][e] *= al[h];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const f4 pv = p_lds[2 * i + pvr];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = (float)vt[i][e];
+#pragma unroll
+                for (int h = 0; h < 4; h++) acc[h][e] = fmaf(pv[h], v, acc[h][e]);
+            }
+        }
+        __syncthreads();
+    };
+
+    auto load_k = [&](int jt, h8* kt) {
+        const int r = min(jt + c, jend - 1);
+        const uint16_t* p = kb + (int64_t)r * kvd + g * 8;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) kt[ks] = ld_h8(p + ks * 32);
+    };
+    auto load_v = [&](int jt, h8* vt) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = min(jt + 2 * i + pvr, jend - 1);
+            vt[i] = ld_h8(vb + (int64_t)r * kvd + pvd);
+        }
+    };
+
+    h8 kt[8], vt[8];
+    if (j0 < jend) {
+        load_k(j0, kt);
+        load_v(j0, vt);
+    }
+    for (int jt = j0; jt < jend; jt += 16) {
+        h8 kn[8], vn[8];
+        const bool more = jt + 16 < jend;
+        if (more) {
+            load_k(jt + 16, kn);
+            load_v(jt + 16, vn);
+        }
+        tile(kt, vt, jt, jend);
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                kt[i] = kn[i];
+                vt[i] = vn[i];
+            }
+        }
+    }
+    if (has_new) {
+        // the appended row: tile row 0 (K lanes with c == 0, V lanes 0..31 at i == 0)
+        const h8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+        const float* kn = a.k_new + seq * a.kn_ss + kh * D;
+        const float* vn = a.v_new + seq * a.kn_ss + kh * D;
+        uint16_t* kdst = a.kc + ((row0 + L - 1) * a.KV + kh) * D;
+        uint16_t* vdst = a.vc + ((row0 + L - 1) * a.KV + kh) * D;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            if (c == 0) {
+                kt[ks] = ld_f32x8_as_h8(kn + ks * 32 + g * 8);
+                st_h8(kdst + ks * 32 + g * 8, kt[ks]);
+            } else {
+                kt[ks] = z8;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) vt[i] = z8;
+        if (pvr == 0) {
+            vt[0] = ld_f32x8_as_h8(vn + pvd);
+            st_h8(vdst + pvd, vt[0]);
+        }
+        tile(kt, vt, L - 1, L);
+    }
+
+    // totals over the lanes holding the same head / dims
+    float l_tot = l_run + __shfl_xor(l_run, 16);
+    l_tot += __shfl_xor(l_tot, 32);
+#pragma unroll
+    for (int h = 0; h < 4; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[h][e] += __shfl_xor(acc[h][e], 32);
+    if (lane < 4) {
+        ml_lds[0][lane] = m_run;
+        ml_lds[1][lane] = l_tot;
+    }
+    __syncthreads();
+
+    if (ns == 1) {
+        if (lane < 32) {
+            const f4 lsum = ml_lds[1];
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                const int head = kh * 4 + h;
+                float* o = a.out + seq * a.o_ss + head * a.o_hs + pvd;
+                const float* z = a.gate ? a.gate + seq * a.g_ss + head * a.g_hs + pvd : nullptr;
+                float y[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    y[e] = acc[h][e] / lsum[h];
+                    if (z) y[e] = gate_mul(y[e], z[e]);
+                }
+                *reinterpret_cast<f4*>(o) = f4{y[0], y[1], y[2], y[3]};
+                *reinterpret_cast<f4*>(o + 4) = f4{y[4], y[5], y[6], y[7]};
+            }
+        }
+        return;
+    }
+
+    float* pp = a.part + (((int64_t)seq * a.KV + kh) * a.max_splits + s) * DEC_PART;
+    if (lane < 4) {
+        pp[lane] = ml_lds[0][lane];
+        pp[4 + lane] = ml_lds[1][lane];
+    }
+    if (lane < 32) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            float* d = pp + 8 + h * D + pvd;
+            *reinterpret_cast<f4*>(d) = f4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+            *reinterpret_cast<f4*>(d + 4) = f4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    uint32_t* cnt = a.cnt + (int64_t)seq * a.KV + kh;
+    if (lane == 0) last_lds = (atomicAdd(cnt, 1u) == (uint32_t)(ns - 1));
+    __syncthreads();
+    if (!last_lds) return;
+    __threadfence();
+
+    // merge the splits in split order: lane = (head lane>>4, dims 16*(lane&15) .. +15)
+    const int h = lane >> 4, d0 = (lane & 15) * 16;
+    const float* pb = a.part + ((int64_t)seq * a.KV + kh) * a.max_splits * DEC_PART;
+    float M = -INFINITY;
+    for (int sp = 0; sp < ns; sp++) M = fmaxf(M, pb[(int64_t)sp * DEC_PART + h]);
+    float Ls = 0.0f, o[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[e] = 0.0f;
+    for (int sp = 0; sp < ns; sp++) {
+        const float* ps = pb + (int64_t)sp * DEC_PART;
+        const float w = exp2f(ps[h] - M);
+        Ls = fmaf(ps[4 + h], w, Ls);
+        const f4* av = reinterpret_cast<const f4*>(ps + 8 + h * D + d0);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const f4 v = av[q4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[q4 * 4 + e] = fmaf(v[e], w, o[q4 * 4 + e]);
+        }
+    }
+    const int head = kh * 4 + h;
+    float* op = a.out + seq * a.o_ss + head * a.o_hs + d0;
+    const float* z = a.gate ? a.gate + seq * a.g_ss + head * a.g_hs + d0 : nullptr;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; q4++) {
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            y[e] = o[q4 * 4 + e] / Ls;
+            if (z) y[e] = gate_mul(y[e], z[q4 * 4 + e]);
+        }
+        *reinterpret_cast<f4*>(op + q4 * 4) = f4{y[0], y[1], y[2], y[3]};
+    }
+    if (lane == 0) atomicExch(cnt, 0u);
+}
+
+}  // namespace bn

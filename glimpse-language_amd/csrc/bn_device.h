@@ -1,0 +1,46 @@
+// Device-side helpers shared by the attention kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bn {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+constexpr int D = 256;                       // head dim (fixed by the architecture)
+constexpr float LOG2E = 1.44269504088896340736f;
+constexpr float QK_SCALE = 0.0625f;          // 1/sqrt(256), exact
+
+// 16 bytes of fp16 at p (16-byte aligned)
+__device__ __forceinline__ h8 ld_h8(const uint16_t* p) {
+    return __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(p));
+}
+__device__ __forceinline__ void st_h8(uint16_t* p, h8 v) {
+    *reinterpret_cast<u4*>(p) = __builtin_bit_cast(u4, v);
+}
+// 8 fp32 at p (16-byte aligned) rounded to fp16, nearest even (v_cvt_f16_f32)
+__device__ __forceinline__ h8 ld_f32x8_as_h8(const float* p) {
+    f4 a = *reinterpret_cast<const f4*>(p);
+    f4 b = *reinterpret_cast<const f4*>(p + 4);
+    h8 r;
+    r[0] = (_Float16)a[0]; r[1] = (_Float16)a[1]; r[2] = (_Float16)a[2]; r[3] = (_Float16)a[3];
+    r[4] = (_Float16)b[0]; r[5] = (_Float16)b[1]; r[6] = (_Float16)b[2]; r[7] = (_Float16)b[3];
+    return r;
+}
+
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// reference gate: a * (1 / (1 + exp(-z)))  (gate_rotate.comp:19-22)
+__device__ __forceinline__ float gate_mul(float a, float z) { return a * (1.0f / (1.0f + expf(-z))); }
+
+}  // namespace bn

@@ -1,0 +1,27 @@
+// Small kernels around the attention call: cache append and workspace fill.
+#pragma once
+#include "bn_device.h"
+
+namespace bn {
+
+// Cache rows [off, off+T) <- fp16(k_new), fp16(v_new); attn_prep.comp:36-39,58 with fp16 storage.
+// n8 = T*KV*256/8 groups of 8 elements; dst points at row off of the cache.
+__global__ __launch_bounds__(256) void append_kernel(const float* __restrict__ kn, const float* __restrict__ vn,
+                                                     uint16_t* __restrict__ kdst, uint16_t* __restrict__ vdst,
+                                                     int64_t n8) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += stride) {
+        st_h8(kdst + i * 8, ld_f32x8_as_h8(kn + i * 8));
+        st_h8(vdst + i * 8, ld_f32x8_as_h8(vn + i * 8));
+    }
+}
+
+// Zero fill with vector stores (no memset node, so it is safe to capture in a graph).
+__global__ __launch_bounds__(256) void fill_zero_kernel(u4* p, int64_t n16, uint8_t* tail, int ntail) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t i = i0; i < n16; i += stride) p[i] = u4{0u, 0u, 0u, 0u};
+    if (i0 < ntail) tail[i0] = 0;
+}
+
+}  // namespace bn

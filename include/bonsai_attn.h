@@ -1,0 +1,144 @@
+/*
+ * bonsai_attn.h - C ABI of the MI355X (gfx950) full-attention path of the Bonsai runtime.
+ *
+ * One call replaces the attention arm of the runtime's layer encoder
+ * (src/bonsai/runtime/model.rs:815-894 in the Glimpse-Language repository), which dispatches
+ *     attn_prep     -> K/V rows appended to the cache at [off, off + T)   (kernels/attn_prep.comp:36-39,58)
+ *     attn_split    -> split-K causal GQA partials                          (kernels/attn_split.comp:9-58)
+ *     attn_combine  -> log-sum-exp merge of the splits                      (kernels/attn_combine.comp:6-21)
+ *     gate_rotate   -> a * sigmoid(gate)  (first half of the kernel)        (kernels/gate_rotate.comp:19-22)
+ * through Cmd::run (src/bonsai/runtime/gpu_vk.rs:843-882, gpu.rs:169-255). Query/key normalisation and
+ * rotary embedding (the rest of attn_prep) happen before the call: q and k_new arrive post-norm, post-RoPE,
+ * or go through bn_attn_prep first.
+ *
+ * Conventions
+ *   - head_dim is 256 and H == 4 * KV (the runtime's fixed GQA 4:1, model.rs:89-129).
+ *   - Query row t sits at position off + t and attends to cache rows [0, off + t + 1) of kv head h / 4
+ *     (causal, including itself and, for several rows, causal among them: attn_split.comp:15).
+ *   - The KV cache is fp16 (IEEE binary16 bits in uint16_t), row-major [cap][KV][256]: element
+ *     ((pos * KV + kh) * 256 + d). The reference stores fp32 in the same position-major layout
+ *     (model.rs:255-267); rows of one prefix stay one contiguous range.
+ *   - k_new / v_new (fp32 [T][KV][256], dense) are rounded to fp16 (nearest even) and written to cache rows
+ *     [off, off + T) by the call. Pass both NULL when those rows are already in the cache.
+ *   - Strides are in elements. Tensors of different calls may alias only as stated.
+ *   - Every call is ordered on `stream` (a hipStream_t; NULL = the default stream), returns without a host
+ *     synchronisation, and allocates nothing: device memory (cache, inputs, outputs, workspace) belongs to
+ *     the caller.
+ *   - A bn_ctx may be used from several threads only if the caller serialises the calls, as the runtime
+ *     does behind its model mutex (src/bonsai/handle.rs:96-103).
+ *   - Errors are status codes; nothing is thrown across the ABI. Argument checks run on the host before any
+ *     launch, so a rejected call has no effect on the device.
+ */
+#ifndef BONSAI_ATTN_H
+#define BONSAI_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BN_HEAD_DIM 256
+#define BN_ABI_VERSION 1
+
+typedef enum bn_status {
+    BN_OK = 0,
+    BN_EINVAL = 1,  /* bad shape, pointer, stride or ratio (replaces the reference's shape asserts, model.rs:671-672) */
+    BN_ENOWS = 2,   /* workspace missing or smaller than the size query returned */
+    BN_ELAUNCH = 3, /* a kernel launch failed (replaces `expect("GPU error")`, gpu_vk.rs:1144) */
+    BN_EDEVICE = 4, /* no usable gfx950 device / HIP runtime error at context creation */
+} bn_status;
+
+typedef struct bn_ctx bn_ctx;
+typedef void* bn_stream; /* hipStream_t */
+
+/* One attention layer call for T query rows of one sequence. */
+typedef struct bn_attn_args {
+    uint32_t T;   /* query rows (1 = decode step, 2..16 = speculative verify, more = prefill) */
+    uint32_t off; /* cache rows before the first query row (the reference's state.len, model.rs:680-681) */
+    uint32_t H;   /* query heads; H == 4 * KV */
+    uint32_t KV;  /* kv heads */
+    uint32_t cap; /* rows allocated in kc / vc; off + T <= cap */
+    uint32_t flags; /* BN_Q_F16: q holds fp16 bits instead of fp32 */
+
+    const void* q; /* [T][H][256] query rows, post-norm and post-RoPE */
+    int64_t q_ts, q_hs; /* token and head strides of q */
+
+    const float* k_new; /* [T][KV][256] fp32, or NULL (rows already cached) */
+    const float* v_new;
+    uint16_t* kc; /* [cap][KV][256] fp16 cache of this layer */
+    uint16_t* vc;
+
+    const float* gate; /* sigmoid-gate logits, element t*g_ts + h*g_hs + d; NULL = no gate */
+    int64_t g_ts, g_hs; /* the runtime's q_proj output [T][H][512] is used in place: gate = qp + 256,
+                           g_ts = 512 * H, g_hs = 512 (gate_rotate.comp:19-20) */
+
+    float* out;         /* [T][H][256] fp32 gated attention output */
+    int64_t o_ts, o_hs;
+
+    void* ws;        /* device workspace, >= bn_attn_workspace_size(args) bytes, zero-filled once before its
+                        first use (bn_workspace_clear); every call leaves it ready for the next one */
+    size_t ws_bytes;
+} bn_attn_args;
+
+#define BN_Q_F16 1u
+
+/* A batch of single-token decodes over sequences of different lengths (one new token each). */
+typedef struct bn_ragged_args {
+    uint32_t nseq;
+    uint32_t H, KV;
+    uint32_t max_len;    /* host-side upper bound of kv_len[i]; sizes the launch */
+    const float* q;      /* [nseq][H][256] fp32 */
+    int64_t q_ss, q_hs;  /* sequence and head strides */
+    const float* k_new;  /* [nseq][KV][256] fp32 appended at row kv_off[i] + kv_len[i] - 1, or NULL */
+    const float* v_new;
+    uint16_t* kc;        /* fp16 rows of all sequences, [rows][KV][256] */
+    uint16_t* vc;
+    const int64_t* kv_off; /* device [nseq]: first cache row of sequence i */
+    const int32_t* kv_len; /* device [nseq]: keys attended by sequence i including the new one, 1..max_len */
+    const float* gate;   /* element i*g_ss + h*g_hs + d, or NULL */
+    int64_t g_ss, g_hs;
+    float* out;          /* element i*o_ss + h*o_hs + d */
+    int64_t o_ss, o_hs;
+    void* ws;
+    size_t ws_bytes;
+} bn_ragged_args;
+
+/* ---- context ---------------------------------------------------------------------------------- */
+bn_status bn_ctx_create(int device, bn_ctx** out);
+void bn_ctx_destroy(bn_ctx* ctx);
+const char* bn_status_str(bn_status s);
+/* Text of the last failed check or launch on this context (empty if none). */
+const char* bn_ctx_last_error(const bn_ctx* ctx);
+int bn_abi_version(void);
+
+/* ---- sizes and checks (pure host code, no device access) ----------------------------------------- */
+size_t bn_attn_workspace_size(const bn_attn_args* a);
+size_t bn_ragged_workspace_size(const bn_ragged_args* a);
+/* kind: 0 forward (any T), 1 decode (T == 1), 2 verify (T <= 16), 3 prefill (any T), 4 append only */
+bn_status bn_attn_check(const bn_attn_args* a, int kind);
+bn_status bn_ragged_check(const bn_ragged_args* a);
+
+/* Zero-fills a workspace on `stream` with a kernel (no memset node: safe inside graph capture). */
+bn_status bn_workspace_clear(bn_ctx* ctx, bn_stream stream, void* ws, size_t bytes);
+
+/* ---- the attention call ------------------------------------------------------------------------- */
+/* Appends k_new/v_new, attends, gates. Chooses the decode, verify or prefill kernel from T
+ * (model.rs:852-855 chooses the reference's split chunk the same way). */
+bn_status bn_attn_forward(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a);
+/* The same call with the kernel fixed; T must fit the kernel (decode: T == 1; verify: T <= 16). */
+bn_status bn_attn_decode(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a);
+bn_status bn_attn_verify(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a);
+bn_status bn_attn_prefill(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a);
+/* Cache append only: rows [off, off + T) of kc/vc from k_new/v_new (attn_prep.comp:36-39,58, fp16 store). */
+bn_status bn_attn_append(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a);
+
+/* Ragged batched decode: no counterpart in the reference (one sequence per model there); each sequence
+ * is the decode call above with its own cache rows. */
+bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_args* a);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

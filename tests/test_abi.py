@@ -1,0 +1,128 @@
+"""The C-ABI library: it loads, exports every symbol include/bonsai_attn.h declares, and its host-side argument
+checks and workspace sizes behave as documented. CPU only: no call here touches a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+from glimpse_language_amd import bonsai_attn as ba
+
+HEADER = os.path.join(ROOT, "include", "bonsai_attn.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(ba.LIB_PATH):
+        import importlib
+        build = importlib.import_module("glimpse_language_amd.build")
+        build.build()
+    return ba.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:bn_status|size_t|void|const char\s*\*|int)\s+(bn_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert set(declared_functions()) == set(ba.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.bn_abi_version() == 1
+
+
+def test_status_strings(lib):
+    for s in range(5):
+        assert lib.bn_status_str(s)
+
+
+def fake(addr):
+    return ctypes.c_void_p(addr)
+
+
+def good_args(T=1, off=100, H=8, KV=2, cap=None):
+    a = ba.AttnArgs()
+    a.T, a.off, a.H, a.KV = T, off, H, KV
+    a.cap = cap if cap is not None else off + T
+    base = 0x100000
+    a.q, a.q_ts, a.q_hs = base, H * 256, 256
+    a.k_new, a.v_new = base + 0x1000, base + 0x2000
+    a.kc, a.vc = base + 0x3000, base + 0x4000
+    a.out, a.o_ts, a.o_hs = base + 0x5000, H * 256, 256
+    a.gate, a.g_ts, a.g_hs = None, 0, 0
+    need = ba.workspace_size(a)
+    a.ws, a.ws_bytes = (base + 0x6000 if need else None), need
+    return a
+
+
+def test_check_accepts_good_shapes(lib):
+    assert ba.check(good_args(), ba.KIND_DECODE) == ba.BN_OK
+    assert ba.check(good_args(T=8, off=2048), ba.KIND_VERIFY) == ba.BN_OK
+    assert ba.check(good_args(T=256, off=512), ba.KIND_PREFILL) == ba.BN_OK
+    assert ba.check(good_args(T=4096, off=0, H=16, KV=4), ba.KIND_FORWARD) == ba.BN_OK
+    assert ba.check(good_args(T=4, off=0), ba.KIND_APPEND) == ba.BN_OK
+
+
+@pytest.mark.parametrize("mutate,kind,status", [
+    (lambda a: setattr(a, "H", 6), ba.KIND_FORWARD, ba.BN_EINVAL),       # not 4:1
+    (lambda a: setattr(a, "KV", 0), ba.KIND_FORWARD, ba.BN_EINVAL),
+    (lambda a: setattr(a, "T", 0), ba.KIND_FORWARD, ba.BN_EINVAL),
+    (lambda a: setattr(a, "cap", a.off + a.T - 1), ba.KIND_FORWARD, ba.BN_EINVAL),  # no room to append
+    (lambda a: setattr(a, "T", 2), ba.KIND_DECODE, ba.BN_EINVAL),        # decode is one row
+    (lambda a: (setattr(a, "T", 17), setattr(a, "cap", 200)), ba.KIND_VERIFY, ba.BN_EINVAL),
+    (lambda a: setattr(a, "kc", 0x100008), ba.KIND_FORWARD, ba.BN_EINVAL),  # misaligned cache
+    (lambda a: setattr(a, "v_new", None), ba.KIND_FORWARD, ba.BN_EINVAL),   # k_new without v_new
+    (lambda a: setattr(a, "out", None), ba.KIND_FORWARD, ba.BN_EINVAL),
+    (lambda a: setattr(a, "o_hs", 255), ba.KIND_FORWARD, ba.BN_EINVAL),
+    (lambda a: setattr(a, "flags", 8), ba.KIND_FORWARD, ba.BN_EINVAL),
+    (lambda a: (setattr(a, "k_new", None), setattr(a, "v_new", None)), ba.KIND_APPEND, ba.BN_EINVAL),
+    (lambda a: setattr(a, "ws_bytes", a.ws_bytes - 16), ba.KIND_FORWARD, ba.BN_ENOWS),
+    (lambda a: setattr(a, "ws", None), ba.KIND_FORWARD, ba.BN_ENOWS),
+])
+def test_check_rejects(lib, mutate, kind, status):
+    a = good_args(T=1, off=5000)   # a decode over 5001 keys needs a workspace
+    assert a.ws_bytes > 0
+    mutate(a)
+    assert ba.check(a, kind) == status
+    assert ba.last_check_error()
+
+
+def test_null_args_rejected(lib):
+    assert lib.bn_attn_check(None, 0) == ba.BN_EINVAL
+    assert lib.bn_ragged_check(None) == ba.BN_EINVAL
+    assert lib.bn_attn_forward(None, None, None) == ba.BN_EINVAL
+
+
+def test_workspace_sizes(lib):
+    # a short decode is one split: no workspace
+    assert ba.workspace_size(good_args(T=1, off=10)) == 0
+    small = ba.workspace_size(good_args(T=1, off=1023))
+    big = ba.workspace_size(good_args(T=1, off=32767))
+    assert 0 < small < big
+    r = ba.RaggedArgs()
+    r.nseq, r.H, r.KV, r.max_len = 32, 16, 4, 32768
+    sz = ba.workspace_size(r)
+    assert sz > 0 and sz % 16 == 0
+    # partial records are (m[4], l[4], acc[4][256]) floats per (sequence, kv head, split)
+    assert (sz - 512) % (4 * (8 + 4 * 256)) == 0
+
+
+def test_ragged_check(lib):
+    r = ba.RaggedArgs()
+    r.nseq, r.H, r.KV, r.max_len = 4, 8, 2, 100
+    base = 0x200000
+    r.q, r.q_ss, r.q_hs = base, 8 * 256, 256
+    r.kc, r.vc = base + 0x1000, base + 0x2000
+    r.kv_off, r.kv_len = base + 0x3000, base + 0x4000
+    r.out, r.o_ss, r.o_hs = base + 0x5000, 8 * 256, 256
+    need = ba.workspace_size(r)
+    r.ws, r.ws_bytes = (base + 0x6000 if need else None), need
+    assert ba.check(r) == ba.BN_OK
+    r.kv_len = None
+    assert ba.check(r) == ba.BN_EINVAL

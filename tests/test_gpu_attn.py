@@ -1,0 +1,193 @@
+"""Parity of the HIP attention path (through the C ABI) with the oracle, on the GPU.
+
+Bar (from the task): outputs within max-abs 2e-3 of the oracle (fp32 accumulate), an identical argmax of
+each output row projected by a fixed random matrix, bit-exact fp16 cache rows after the append, and
+bit-identical results across repeated runs.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import workload
+from glimpse_language_amd import bonsai_attn as ba
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3  # max-abs tolerance against the oracle
+
+
+def to_dev(torch, inp):
+    d = {}
+    for k in ("q", "k_new", "v_new", "gate"):
+        d[k] = None if inp[k] is None else torch.from_numpy(np.ascontiguousarray(inp[k])).cuda()
+    d["kc"] = torch.from_numpy(inp["kc"].view(np.int16).copy()).cuda()
+    d["vc"] = torch.from_numpy(inp["vc"].view(np.int16).copy()).cuda()
+    return d
+
+
+def run(gpu, inp, kind=ba.KIND_FORWARD, append=True, dev=None):
+    torch, ctx, ws = gpu
+    d = dev or to_dev(torch, inp)
+    out = ba.attention(ctx, ws, d["q"], d["kc"], d["vc"], inp["off"], k_new=d["k_new"] if append else None,
+                       v_new=d["v_new"] if append else None, gate=d["gate"], kind=kind)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), d
+
+
+def cache_np(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def assert_parity(out, ref, H, what=""):
+    err = float(np.max(np.abs(out - ref)))
+    assert err <= TOL, f"{what} max-abs {err:.3e} > {TOL}"
+    R = workload.projection(H)
+    a, b = workload.projected_argmax(out, R), workload.projected_argmax(ref, R)
+    assert np.array_equal(a, b), f"{what} projected argmax differs in {np.sum(a != b)} rows"
+    return err
+
+
+def check_case(gpu, inp, kind=ba.KIND_FORWARD, rows=None):
+    out, d = run(gpu, inp, kind)
+    ref, kc_ref, vc_ref = workload.expected(inp, rows=rows)
+    T = inp["T"]
+    got = out if rows is None else out[list(rows)]
+    err = assert_parity(got, ref, inp["H"], f"T={T} off={inp['off']}")
+    assert np.array_equal(cache_np(d["kc"]), kc_ref), "K cache differs after the append"
+    assert np.array_equal(cache_np(d["vc"]), vc_ref), "V cache differs after the append"
+    # repeat on the updated cache without the append: same bits
+    out2, _ = run(gpu, inp, kind, append=False, dev=d)
+    assert np.array_equal(out, out2), "repeat run not bit-identical"
+    return err
+
+
+@pytest.mark.parametrize("L", [1, 2, 15, 16, 17, 63, 64, 65, 100, 1000, 1024, 4097, 9000])
+def test_decode_lengths(gpu, L):
+    inp = workload.layer(workload.SEED_BASE + L, T=1, off=L - 1, H=8, KV=2)
+    check_case(gpu, inp, ba.KIND_DECODE)
+
+
+def test_decode_1k_workload(gpu):
+    inp = workload.layer(workload.SEED_BASE + 0, **{k: v for k, v in workload.WORKLOADS["decode_1k"].items()})
+    err = check_case(gpu, inp, ba.KIND_DECODE)
+    print(f"decode_1k max-abs {err:.3e}")
+
+
+def test_decode_4b_heads_no_gate(gpu):
+    inp = workload.layer(77, T=1, off=3000, H=16, KV=4, gate=False)
+    check_case(gpu, inp, ba.KIND_DECODE)
+
+
+def test_decode_without_append_reads_cache_row(gpu):
+    inp = workload.layer(78, T=1, off=500, H=8, KV=2)
+    kc, vc = inp["kc"].copy(), inp["vc"].copy()
+    oracle.append(inp["k_new"], inp["v_new"], kc, vc, inp["off"])
+    inp2 = dict(inp, kc=kc, vc=vc)
+    out, _ = run(gpu, inp2, ba.KIND_DECODE, append=False)
+    ref = oracle.attend(inp["q"], kc, vc, inp["off"], inp["gate"])
+    assert_parity(out, ref, 8)
+
+
+def test_gate_in_place_from_qproj(gpu):
+    torch, ctx, ws = gpu
+    inp = workload.layer(79, T=1, off=700, H=8, KV=2)
+    qp = oracle.normal(79, 9, (1, 8, 512))
+    d = to_dev(torch, inp)
+    qp_d = torch.from_numpy(qp).cuda()
+    out = ba.attention(ctx, ws, d["q"], d["kc"], d["vc"], inp["off"], k_new=d["k_new"], v_new=d["v_new"],
+                       gate=qp_d[:, :, 256:], g_strides=(8 * 512, 512))
+    torch.cuda.synchronize()
+    ref, _, _ = workload.expected(dict(inp, gate=qp[:, :, 256:]))
+    assert_parity(out.cpu().numpy(), ref, 8)
+
+
+def test_verify_8_workload(gpu):
+    inp = workload.layer(workload.SEED_BASE + 2, **workload.WORKLOADS["verify_8"])
+    check_case(gpu, inp, ba.KIND_VERIFY)
+
+
+@pytest.mark.parametrize("T,off", [(2, 0), (3, 17), (16, 1000), (5, 4095)])
+def test_verify_shapes(gpu, T, off):
+    inp = workload.layer(900 + T + off, T=T, off=off, H=8, KV=2)
+    check_case(gpu, inp, ba.KIND_VERIFY)
+
+
+def test_verify_rows_equal_decodes(gpu):
+    """Row t of a verify call equals a decode at off+t: the equivalence the runtime's accept relies on."""
+    inp = workload.layer(31, T=6, off=800, H=8, KV=2)
+    out, d = run(gpu, inp, ba.KIND_VERIFY)
+    torch, ctx, ws = gpu
+    for t in range(6):
+        o = ba.attention(ctx, ws, d["q"][t:t + 1], d["kc"], d["vc"], inp["off"] + t,
+                         gate=d["gate"][t:t + 1], kind=ba.KIND_DECODE)
+        torch.cuda.synchronize()
+        assert np.max(np.abs(o.cpu().numpy()[0] - out[t])) <= 1e-5
+
+
+def test_prefill_prefix_workload(gpu):
+    inp = workload.layer(workload.SEED_BASE + 1, **workload.WORKLOADS["prefill_prefix"])
+    err = check_case(gpu, inp, ba.KIND_PREFILL)
+    print(f"prefill_prefix max-abs {err:.3e}")
+
+
+@pytest.mark.parametrize("T,off,H,KV", [(17, 0, 4, 1), (33, 5, 8, 2), (100, 300, 16, 4)])
+def test_prefill_shapes(gpu, T, off, H, KV):
+    inp = workload.layer(1000 + T + off, T=T, off=off, H=H, KV=KV)
+    check_case(gpu, inp, ba.KIND_PREFILL)
+
+
+def test_prefill_4k_workload_sampled_rows(gpu):
+    """Full 4096-row prefill on the GPU; the oracle checks a spread of rows (decode-equivalent rows)."""
+    inp = workload.layer(workload.SEED_BASE + 3, **workload.WORKLOADS["prefill_4k"])
+    rows = sorted(set([0, 1, 2, 63, 64, 127, 128, 1000, 2047, 2048, 3001, 4094, 4095] +
+                      list(np.random.default_rng(5).integers(0, 4096, 20))))
+    err = check_case(gpu, inp, ba.KIND_PREFILL, rows=rows)
+    print(f"prefill_4k sampled rows max-abs {err:.3e}")
+
+
+def make_ragged(seed, nseq, H, KV, lo, hi):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, size=nseq).astype(np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    rows = int(lens.sum())
+    kc = oracle.f32_to_f16(oracle.rms_rows(oracle.normal(seed, 2, (rows, KV, 256))))
+    vc = oracle.f32_to_f16(oracle.normal(seed, 3, (rows, KV, 256)))
+    q = oracle.rms_rows(oracle.normal(seed, 1, (nseq, H, 256)))
+    k_new = oracle.rms_rows(oracle.normal(seed, 4, (nseq, KV, 256)))
+    v_new = oracle.normal(seed, 5, (nseq, KV, 256))
+    z = oracle.normal(seed, 6, (nseq, H, 256))
+    return lens, offs, kc, vc, q, k_new, v_new, z
+
+
+@pytest.mark.parametrize("nseq,lo,hi", [(1, 1, 1), (7, 1, 300), (32, 1024, 4096), (5, 4000, 20000)])
+def test_ragged_decode(gpu, nseq, lo, hi):
+    torch, ctx, ws = gpu
+    H, KV = 16, 4
+    lens, offs, kc, vc, q, k_new, v_new, z = make_ragged(nseq * 1000 + hi, nseq, H, KV, lo, hi)
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    for i in range(nseq):  # the new row of sequence i goes to its last row
+        r = offs[i] + lens[i] - 1
+        kc_ref[r] = k_new[i].astype(np.float16).view(np.uint16)
+        vc_ref[r] = v_new[i].astype(np.float16).view(np.uint16)
+    ref = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens, z)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    kc_d, vc_d = t(kc.view(np.int16)), t(vc.view(np.int16))
+    out = ba.decode_ragged(ctx, ws, t(q), kc_d, vc_d, t(offs), t(lens), int(lens.max()), k_new=t(k_new),
+                           v_new=t(v_new), gate=t(z))
+    torch.cuda.synchronize()
+    assert_parity(out.cpu().numpy(), ref, H, "ragged")
+    assert np.array_equal(cache_np(kc_d), kc_ref)
+    assert np.array_equal(cache_np(vc_d), vc_ref)
+
+
+def test_bad_arguments_do_not_launch(gpu):
+    torch, ctx, ws = gpu
+    inp = workload.layer(5, T=2, off=10, H=8, KV=2)
+    d = to_dev(torch, inp)
+    with pytest.raises(ba.BonsaiAttnError) as e:
+        ba.attention(ctx, ws, d["q"], d["kc"], d["vc"], 10, kind=ba.KIND_DECODE)  # T=2 is not a decode
+    assert e.value.status == ba.BN_EINVAL
+    a = ba.attn_args(1, 5000, 8, 2, 5001, d["q"], d["kc"], d["vc"], d["q"])
+    with pytest.raises(ba.BonsaiAttnError) as e:
+        ctx.call("bn_attn_decode", a)  # needs a workspace
+    assert e.value.status == ba.BN_ENOWS

@@ -1,0 +1,297 @@
+"""Pins the CPU oracle before it is trusted as the checker (CPU only).
+
+The reference ships no kernel-level vectors for this path, and its shaders cannot be run here (no Rust,
+glslc or Vulkan). Each oracle function is therefore pinned by what the mathematics fixes:
+  - attention: float64 brute-force softmax(q k^T / 16) v over the causal window, plus invariants (split
+    independence, L = 1, equal scores, a dominant key, causality, GQA head mapping, decode/verify equivalence);
+  - fp16 storage: numpy's IEEE binary16 conversion, bit for bit, including subnormals, ties and overflow;
+  - gate: sigmoid(0) = 1/2 exactly;
+  - attn_prep: RMS-norm closed form, text-position mRoPE = standard rotate-half RoPE on 64 dims, sin/cos;
+  - gate_rotate: the Sylvester Hadamard matrix (scipy) in float64.
+"""
+import numpy as np
+import pytest
+import scipy.linalg
+
+import oracle
+import workload
+
+D = 256
+
+
+def brute(q, kc, vc, off, gate=None):
+    """float64 closed form: out[t,h] = softmax_j<off+t+1 (q.k_j / 16) . v_j, then * sigmoid(gate)."""
+    kf = oracle.f16_to_f32(kc).astype(np.float64)
+    vf = oracle.f16_to_f32(vc).astype(np.float64)
+    T, H = q.shape[0], q.shape[1]
+    out = np.empty((T, H, D))
+    for t in range(T):
+        n = off + t + 1
+        for h in range(H):
+            kh = h // 4
+            s = kf[:n, kh, :] @ q[t, h].astype(np.float64) / 16.0
+            p = np.exp(s - s.max())
+            out[t, h] = (p @ vf[:n, kh, :]) / p.sum()
+    if gate is not None:
+        out = out / (1.0 + np.exp(-gate.astype(np.float64)))
+    return out
+
+
+# ---------------------------------------------------------------------------------------------------------
+# fp16 storage
+
+def test_f32_to_f16_matches_ieee_rne():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * np.float32(3.0),
+        (rng.standard_normal(50000) * 1e-5).astype(np.float32),          # subnormal range of fp16
+        (rng.standard_normal(20000) * 3e4).astype(np.float32),           # near overflow
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, -65520.0, 1e9, -1e9, np.inf, -np.inf,
+                  2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0000001, 2.0 ** -26, 2.0 ** -14, 2.0 ** -14 * 0.9999],
+                 dtype=np.float32),
+    ])
+    # exact ties between neighbouring fp16 values: (a + b) / 2 is an fp32 number
+    a = np.arange(0x0001, 0x7BFF, 7, dtype=np.uint16)
+    lo = a.view(np.float16).astype(np.float32)
+    hi = (a + 1).view(np.float16).astype(np.float32)
+    x = np.concatenate([x, (lo + hi) / np.float32(2.0), -(lo + hi) / np.float32(2.0)])
+    ours = oracle.f32_to_f16(x)
+    ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, ref)
+    nan = oracle.f32_to_f16(np.array([np.nan], dtype=np.float32))[0]
+    assert (nan & 0x7C00) == 0x7C00 and (nan & 0x3FF) != 0
+
+
+def test_f16_to_f32_exact():
+    h = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    ours = oracle.f16_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    finite = np.isfinite(ref)
+    assert np.array_equal(ours[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    assert np.array_equal(np.isinf(ours), np.isinf(ref))
+
+
+def test_append_rows():
+    inp = workload.layer(5, T=3, off=4, H=4, KV=1)
+    kc, vc = inp["kc"].copy(), inp["vc"].copy()
+    oracle.append(inp["k_new"], inp["v_new"], kc, vc, 4)
+    assert np.array_equal(kc[4:7], inp["k_new"].astype(np.float16).view(np.uint16))
+    assert np.array_equal(vc[4:7], inp["v_new"].astype(np.float16).view(np.uint16))
+    assert np.array_equal(kc[:4], inp["kc"][:4])
+
+
+def test_generator_distribution():
+    x = oracle.normal(123, 0, (400000,)).astype(np.float64)
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
+    assert not np.array_equal(oracle.normal(123, 0, (8,)), oracle.normal(123, 1, (8,)))
+    assert np.array_equal(oracle.normal(7, 3, (5,)), oracle.normal(7, 3, (5,)))
+    r = oracle.rms_rows(oracle.normal(9, 0, (10, D)))
+    assert np.allclose(np.sqrt((r.astype(np.float64) ** 2).mean(axis=1)), 1.0, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# attention
+
+@pytest.mark.parametrize("T,off,H,KV,chunk", [
+    (1, 0, 4, 1, 0), (1, 130, 8, 2, 0), (1, 511, 8, 2, 64), (5, 77, 8, 2, 0), (40, 100, 16, 4, 0),
+    (24, 0, 4, 1, 16), (3, 600, 4, 1, 512)])
+def test_attend_matches_float64_closed_form(T, off, H, KV, chunk):
+    inp = workload.layer(11 + T + off, T=T, off=off, H=H, KV=KV)
+    out, kc, vc = workload.expected(inp, chunk=chunk)
+    ref = brute(inp["q"], kc, vc, off, inp["gate"])
+    assert np.max(np.abs(out - ref)) < 2e-6
+
+
+def test_attend_ungated_closed_form():
+    inp = workload.layer(3, T=6, off=50, H=8, KV=2, gate=False)
+    out, kc, vc = workload.expected(inp)
+    assert np.max(np.abs(out - brute(inp["q"], kc, vc, 50))) < 2e-6
+
+
+def test_split_count_does_not_change_result():
+    inp = workload.layer(21, T=4, off=700, H=4, KV=1)
+    outs = [workload.expected(inp, chunk=c)[0] for c in (16, 64, 512, 4096)]
+    for o in outs[1:]:
+        assert np.max(np.abs(o - outs[0])) < 1e-6
+
+
+def test_single_key_returns_v_row_exactly():
+    inp = workload.layer(4, T=1, off=0, H=8, KV=2, gate=False)
+    out, kc, vc = workload.expected(inp)
+    v = oracle.f16_to_f32(vc[0])  # [KV][256]
+    for h in range(8):
+        assert np.array_equal(out[0, h], v[h // 4])
+
+
+def test_equal_scores_give_mean_of_v():
+    inp = workload.layer(6, T=1, off=299, H=4, KV=1, gate=False)
+    inp["q"][:] = 0.0
+    out, kc, vc = workload.expected(inp)
+    mean = oracle.f16_to_f32(vc[:300, 0]).astype(np.float64).mean(axis=0)
+    assert np.max(np.abs(out[0] - mean)) < 1e-6
+
+
+def test_dominant_key_selects_its_value():
+    inp = workload.layer(8, T=1, off=199, H=4, KV=1, gate=False)
+    kc0 = inp["kc"]
+    j = 123
+    kj = oracle.f16_to_f32(kc0[j, 0])
+    inp["q"][0, 2] = 8.0 * kj  # score of key j = 8*|k_j|^2/16 = 128; the rest are far below
+    out, kc, vc = workload.expected(inp)
+    assert np.max(np.abs(out[0, 2] - oracle.f16_to_f32(vc[j, 0]))) < 1e-6
+
+
+def test_causal_rows_ignore_later_keys():
+    inp = workload.layer(12, T=6, off=30, H=4, KV=1)
+    out, kc, vc = workload.expected(inp)
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[33:] = oracle.f32_to_f16(oracle.normal(99, 0, kc2[33:].shape))
+    vc2[33:] = oracle.f32_to_f16(oracle.normal(98, 0, vc2[33:].shape))
+    out2 = oracle.attend(inp["q"], kc2, vc2, 30, inp["gate"])
+    assert np.array_equal(out[:3], out2[:3])  # rows 0..2 see keys < 33 only
+    assert not np.array_equal(out[3:], out2[3:])
+
+
+def test_gqa_head_mapping():
+    inp = workload.layer(13, T=2, off=40, H=8, KV=2)
+    out, kc, vc = workload.expected(inp)
+    kc2 = kc.copy()
+    kc2[:, 1] = oracle.f32_to_f16(oracle.rms_rows(oracle.normal(77, 0, (kc.shape[0], D))))
+    out2 = oracle.attend(inp["q"], kc2, vc, 40, inp["gate"])
+    assert np.array_equal(out[:, :4], out2[:, :4])     # heads 0..3 read kv head 0
+    assert not np.any(np.all(out[:, 4:] == out2[:, 4:], axis=-1))
+
+
+def test_rows_equal_single_row_decodes_bit_exactly():
+    inp = workload.layer(14, T=7, off=300, H=8, KV=2)
+    full, kc, vc = workload.expected(inp, chunk=64)
+    rows, _, _ = workload.expected(inp, chunk=64, rows=range(7))
+    assert np.array_equal(full, rows)
+
+
+def test_gate_zero_halves_exactly():
+    inp = workload.layer(15, T=3, off=20, H=4, KV=1)
+    inp["gate"][:] = 0.0
+    gated, kc, vc = workload.expected(inp)
+    plain = oracle.attend(inp["q"], kc, vc, 20, None)
+    assert np.array_equal(gated, plain * np.float32(0.5))
+
+
+def test_gate_read_in_place_from_qproj_layout():
+    """gate = q_proj output [T][H][512] + 256 (gate_rotate.comp:19-20), read through strides."""
+    inp = workload.layer(16, T=3, off=9, H=8, KV=2)
+    qp = oracle.normal(55, 0, (3, 8, 512))
+    out_view, kc, vc = workload.expected(dict(inp, gate=qp[:, :, 256:]))
+    out_copy = oracle.attend(inp["q"], kc, vc, 9, np.ascontiguousarray(qp[:, :, 256:]))
+    assert np.array_equal(out_view, out_copy)
+
+
+def test_ragged_equals_per_sequence():
+    rng = np.random.default_rng(3)
+    lens = rng.integers(1, 200, size=5).astype(np.int32)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    rows = int(lens.sum())
+    kc = oracle.f32_to_f16(oracle.rms_rows(oracle.normal(1, 2, (rows, 2, D))))
+    vc = oracle.f32_to_f16(oracle.normal(1, 3, (rows, 2, D)))
+    q = oracle.rms_rows(oracle.normal(1, 1, (5, 8, D)))
+    z = oracle.normal(1, 6, (5, 8, D))
+    out = oracle.decode_ragged(q, kc, vc, offs, lens, z)
+    for i in range(5):
+        o, n = offs[i], lens[i]
+        ref = oracle.attend(q[i:i + 1], kc[o:o + n], vc[o:o + n], n - 1, z[i:i + 1])
+        assert np.array_equal(out[i], ref[0])
+
+
+def test_threads_do_not_change_bits():
+    inp = workload.layer(17, T=9, off=600, H=8, KV=2)
+    a = workload.expected(inp, nthreads=1)[0]
+    b = workload.expected(inp, nthreads=4)[0]
+    assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------------------------------------------------
+# attn_prep
+
+def _inv_freq(theta=1e7, rot=64):
+    i = np.arange(rot // 2, dtype=np.float32)
+    return (np.float32(1.0) / np.power(np.float32(theta), (2 * i).astype(np.float32) / np.float32(rot))).astype(np.float32)
+
+
+def test_sincos_accuracy():
+    xs = np.concatenate([np.linspace(-10, 10, 2001), np.linspace(0, 4096, 4001), [1e4, 3e4, 6e4]]).astype(np.float32)
+    for x in xs:
+        s, c = oracle.sincos(x)
+        assert abs(s - np.sin(np.float64(x))) < 3e-7 * max(1.0, 1.0) + 2e-7
+        assert abs(c - np.cos(np.float64(x))) < 5e-7
+
+
+def test_prep_norm_and_text_rope():
+    T, H, KV, off = 5, 8, 2, 3
+    qp = oracle.normal(30, 0, (T, H, 512)) * np.float32(2.5)
+    kp = oracle.normal(30, 1, (T, KV, D))
+    vp = oracle.normal(30, 2, (T, KV, D))
+    qn = (1.0 + 0.1 * oracle.normal(30, 3, (D,))).astype(np.float32)
+    kn = (1.0 + 0.1 * oracle.normal(30, 4, (D,))).astype(np.float32)
+    p = np.arange(100, 100 + T, dtype=np.int32)
+    pos = np.stack([p, p, p])  # text tokens: all three mRoPE rows equal
+    inv = _inv_freq()
+    kc = np.zeros((off + T, KV, D), np.uint16)
+    vc = np.zeros_like(kc)
+    qout = oracle.prep(qp, kp, vp, qn, kn, pos, inv, kc, vc, off)
+
+    def ref(x, w, t):
+        x = x.astype(np.float64)
+        y = x / np.sqrt((x ** 2).mean() + 1e-6) * w
+        ang = p[t] * inv.astype(np.float64)
+        c, s = np.cos(ang), np.sin(ang)
+        a, b = y[:32].copy(), y[32:64].copy()
+        y[:32] = a * c - b * s
+        y[32:64] = b * c + a * s
+        return y
+
+    for t in range(T):
+        for h in range(H):
+            assert np.max(np.abs(qout[t, h] - ref(qp[t, h, :256], qn, t))) < 2e-5
+        for kh in range(KV):
+            kref = ref(kp[t, kh], kn, t)
+            got = oracle.f16_to_f32(kc[off + t, kh])
+            assert np.max(np.abs(got - kref) / np.maximum(np.abs(kref), 1e-3)) < 1.5e-3
+            assert np.array_equal(vc[off + t, kh], vp[t, kh].astype(np.float16).view(np.uint16))
+
+
+def test_prep_mrope_sections_select_position_rows():
+    """Interleaved mRoPE: pair i uses the h row if i%3==1 and i<33, the w row if i%3==2 and i<33, else t."""
+    T, H, KV = 1, 4, 1
+    qp = oracle.normal(31, 0, (T, H, 512))
+    kp = oracle.normal(31, 1, (T, KV, D))
+    vp = oracle.normal(31, 2, (T, KV, D))
+    ones = np.ones(D, np.float32)
+    inv = _inv_freq()
+    pos = np.array([[7], [900], [40000]], np.int32)
+    kc = np.zeros((1, KV, D), np.uint16)
+    vc = np.zeros_like(kc)
+    qout = oracle.prep(qp, kp, vp, ones, ones, pos, inv, kc, vc, 0)
+    x = qp[0, 0, :256].astype(np.float64)
+    y = x / np.sqrt((x ** 2).mean() + 1e-6)
+    for i in range(32):
+        sel = 1 if (i % 3 == 1 and i < 33) else (2 if (i % 3 == 2 and i < 33) else 0)
+        ang = float(np.float32(pos[sel, 0]) * inv[i])  # the angle is an fp32 product (attn_prep.comp:52)
+        assert abs(qout[0, 0, i] - (y[i] * np.cos(ang) - y[i + 32] * np.sin(ang))) < 3e-5
+        assert abs(qout[0, 0, i + 32] - (y[i + 32] * np.cos(ang) + y[i] * np.sin(ang))) < 3e-5
+    assert np.max(np.abs(qout[0, 0, 64:] - y[64:])) < 1e-5  # dims past ROT are only normalised
+
+
+def test_gate_rotate_is_scaled_sylvester_hadamard():
+    T, H = 2, 8
+    W = H * 256
+    attn = oracle.normal(40, 0, (T, W))
+    qp = oracle.normal(40, 1, (T, 2 * W))
+    signs = np.where(oracle.normal(40, 2, (W,)) > 0, 1.0, -1.0).astype(np.float32)
+    xr = oracle.gate_rotate(attn, qp, signs)
+    Hm = scipy.linalg.hadamard(512).astype(np.float64) / np.sqrt(512.0)
+    for t in range(T):
+        g = qp[t].reshape(H, 512)[:, 256:].reshape(W).astype(np.float64)
+        x = attn[t].astype(np.float64) / (1.0 + np.exp(-g)) * signs
+        ref = np.concatenate([Hm @ x[b:b + 512] for b in range(0, W, 512)])
+        assert np.max(np.abs(xr[t] - ref)) < 2e-5

@@ -1,0 +1,55 @@
+"""Seeded synthetic attention-layer inputs shared by the tests (drawn with the oracle's generator).
+
+Q and K rows are RMS-normalised N(0,1) samples (post-QK-norm, post-RoPE), V and the gate logits are N(0,1);
+K/V cache rows are stored as fp16. Seeds follow the workload list: 0xB0A5A100 + workload index.
+"""
+import numpy as np
+
+import oracle
+
+D = 256
+SEED_BASE = 0xB0A5A100
+PROJ_SEED = 0xA5A5
+
+# (name, H, KV, T, off): the single-GPU workloads the library is checked on
+WORKLOADS = {
+    "decode_1k": dict(H=8, KV=2, T=1, off=1023),       # one query vs 1024 keys (incl. the new one)
+    "prefill_prefix": dict(H=8, KV=2, T=256, off=512),  # user turn over a cached 512-row prefix
+    "verify_8": dict(H=8, KV=2, T=8, off=2048),         # 8 drafts vs 2048 cached rows
+    "prefill_4k": dict(H=16, KV=4, T=4096, off=0),      # 4B-scale 4096-row causal prefill
+}
+
+
+def layer(seed, T, off, H, KV, cap=None, gate=True):
+    """Inputs of one attention call. kc/vc rows [off, off+T) hold filler the call overwrites."""
+    cap = cap or off + T
+    q = oracle.rms_rows(oracle.normal(seed, 1, (T, H, D)))
+    kc = oracle.f32_to_f16(oracle.rms_rows(oracle.normal(seed, 2, (cap, KV, D))))
+    vc = oracle.f32_to_f16(oracle.normal(seed, 3, (cap, KV, D)))
+    k_new = oracle.rms_rows(oracle.normal(seed, 4, (T, KV, D)))
+    v_new = oracle.normal(seed, 5, (T, KV, D))
+    z = oracle.normal(seed, 6, (T, H, D)) if gate else None
+    return dict(q=q, kc=kc, vc=vc, k_new=k_new, v_new=v_new, gate=z, T=T, off=off, H=H, KV=KV, cap=cap)
+
+
+def expected(inp, chunk=0, nthreads=0, rows=None):
+    """Oracle output after appending k_new/v_new; rows (optional) selects query rows (decode-equivalent)."""
+    kc, vc = inp["kc"].copy(), inp["vc"].copy()
+    oracle.append(inp["k_new"], inp["v_new"], kc, vc, inp["off"])
+    if rows is None:
+        out = oracle.attend(inp["q"], kc, vc, inp["off"], inp["gate"], chunk, nthreads)
+        return out, kc, vc
+    outs = []
+    for t in rows:
+        g = None if inp["gate"] is None else inp["gate"][t:t + 1]
+        outs.append(oracle.attend(inp["q"][t:t + 1], kc, vc, inp["off"] + t, g, chunk, nthreads)[0])
+    return np.stack(outs), kc, vc
+
+
+def projection(H):
+    return oracle.normal(PROJ_SEED, 0, (H * D, 128)).astype(np.float64)
+
+
+def projected_argmax(out, R):
+    T = out.shape[0]
+    return np.argmax(out.reshape(T, -1).astype(np.float64) @ R, axis=1)
