@@ -59,9 +59,8 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeArgs a) {
     if (s >= ns) return;
     const int j0 = s * a.chunk;
     const int j1 = min(L, j0 + a.chunk);
-    const bool append = a.k_new != nullptr;
-    const bool has_new = append && j1 == L;   // this split owns the appended row L-1
-    const int jend = has_new ? L - 1 : j1;    // keys [j0, jend) come from the cache
+    const bool has_new = a.k_new != nullptr && j1 == L;  // this split owns the appended row L-1
+    const int tl = j0 + (j1 - j0 - 1) / 16 * 16;          // first key of the split's last (maybe partial) tile
     const int64_t kvd = (int64_t)a.KV * D;
     const uint16_t* kb = a.kc + (row0 * a.KV + kh) * D;
     const uint16_t* vb = a.vc + (row0 * a.KV + kh) * D;
@@ -137,8 +136,9 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeArgs a) {
         __syncthreads();
     };
 
+    // rows past the split end are clamped to its last row (in bounds; their scores are masked)
     auto load_k = [&](int jt, h8* kt) {
-        const int r = min(jt + c, jend - 1);
+        const int r = min(jt + c, j1 - 1);
         const uint16_t* p = kb + (int64_t)r * kvd + g * 8;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) kt[ks] = ld_h8(p + ks * 32);
@@ -146,56 +146,50 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeArgs a) {
     auto load_v = [&](int jt, h8* vt) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int r = min(jt + 2 * i + pvr, jend - 1);
+            const int r = min(jt + 2 * i + pvr, j1 - 1);
             vt[i] = ld_h8(vb + (int64_t)r * kvd + pvd);
         }
     };
 
+    // full tiles [j0, tl) with the next tile's loads in flight, then the last tile [tl, j1)
     h8 kt[8], vt[8];
-    if (j0 < jend) {
-        load_k(j0, kt);
-        load_v(j0, vt);
-    }
-    for (int jt = j0; jt < jend; jt += 16) {
+    load_k(j0, kt);
+    load_v(j0, vt);
+    for (int jt = j0; jt < tl; jt += 16) {
         h8 kn[8], vn[8];
-        const bool more = jt + 16 < jend;
-        if (more) {
-            load_k(jt + 16, kn);
-            load_v(jt + 16, vn);
-        }
-        tile(kt, vt, jt, jend);
-        if (more) {
+        load_k(jt + 16, kn);
+        load_v(jt + 16, vn);
+        tile(kt, vt, jt, j1);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                kt[i] = kn[i];
-                vt[i] = vn[i];
-            }
+        for (int i = 0; i < 8; i++) {
+            kt[i] = kn[i];
+            vt[i] = vn[i];
         }
     }
     if (has_new) {
-        // the appended row: tile row 0 (K lanes with c == 0, V lanes 0..31 at i == 0)
-        const h8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+        // row L-1 of the last tile comes from k_new / v_new (fp16, nearest even) and is stored to the cache,
+        // so a call that appends and one that finds the row cached produce the same bits
+        const int rn = L - 1 - tl;  // tile row of the new key
         const float* kn = a.k_new + seq * a.kn_ss + kh * D;
         const float* vn = a.v_new + seq * a.kn_ss + kh * D;
         uint16_t* kdst = a.kc + ((row0 + L - 1) * a.KV + kh) * D;
         uint16_t* vdst = a.vc + ((row0 + L - 1) * a.KV + kh) * D;
+        if (c == rn) {
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            if (c == 0) {
+            for (int ks = 0; ks < 8; ks++) {
                 kt[ks] = ld_f32x8_as_h8(kn + ks * 32 + g * 8);
                 st_h8(kdst + ks * 32 + g * 8, kt[ks]);
-            } else {
-                kt[ks] = z8;
             }
         }
 #pragma unroll
-        for (int i = 0; i < 8; i++) vt[i] = z8;
-        if (pvr == 0) {
-            vt[0] = ld_f32x8_as_h8(vn + pvd);
-            st_h8(vdst + pvd, vt[0]);
+        for (int i = 0; i < 8; i++) {
+            if (2 * i + pvr == rn) {
+                vt[i] = ld_f32x8_as_h8(vn + pvd);
+                st_h8(vdst + pvd, vt[i]);
+            }
         }
-        tile(kt, vt, L - 1, L);
     }
+    tile(kt, vt, tl, j1);
 
     // totals over the lanes holding the same head / dims
     float l_tot = l_run + __shfl_xor(l_run, 16);

@@ -77,8 +77,10 @@ typedef struct bn_attn_args {
     float* out;         /* [T][H][256] fp32 gated attention output */
     int64_t o_ts, o_hs;
 
-    void* ws;        /* device workspace, >= bn_attn_workspace_size(args) bytes, zero-filled once before its
-                        first use (bn_workspace_clear); every call leaves it ready for the next one */
+    void* ws;        /* device workspace, >= bn_attn_workspace_size(args) bytes (0 = none needed). Its first
+                        256 KiB hold split counters: zero-fill it once before its first use (bn_workspace_clear);
+                        every call leaves the counters at zero, so one workspace serves calls of any shape.
+                        Calls that overlap in time on one workspace race. */
     size_t ws_bytes;
 } bn_attn_args;
 

@@ -180,6 +180,28 @@ def test_ragged_decode(gpu, nseq, lo, hi):
     assert np.array_equal(cache_np(vc_d), vc_ref)
 
 
+def test_workspace_reused_across_shapes(gpu):
+    """One workspace serves calls of different shapes in turn: the split counters stay at zero between calls
+    and no call's partial records overlap them."""
+    torch, ctx, _ = gpu
+    ws = ba.Workspace(ctx, "cuda")
+    ws.get(64 << 20)  # large enough for every call below, so the same bytes are reused
+    for seed, (T, off, H, KV) in enumerate([(100, 700, 8, 2), (1, 8999, 8, 2), (1, 3000, 16, 4), (7, 4000, 16, 4)]):
+        inp = workload.layer(4242 + seed, T=T, off=off, H=H, KV=KV)
+        d = to_dev(torch, inp)
+        out = ba.attention(ctx, ws, d["q"], d["kc"], d["vc"], off, k_new=d["k_new"], v_new=d["v_new"],
+                           gate=d["gate"])
+        torch.cuda.synchronize()
+        ref, _, _ = workload.expected(inp)
+        assert_parity(out.cpu().numpy(), ref, H, f"reuse T={T} off={off}")
+    lens, offs, kc, vc, q, k_new, v_new, z = make_ragged(99, 32, 16, 4, 1024, 4096)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out = ba.decode_ragged(ctx, ws, t(q), t(kc.view(np.int16)), t(vc.view(np.int16)), t(offs), t(lens),
+                           int(lens.max()))
+    torch.cuda.synchronize()
+    assert_parity(out.cpu().numpy(), oracle.decode_ragged(q, kc, vc, offs, lens), 16, "reuse ragged")
+
+
 def test_bad_arguments_do_not_launch(gpu):
     torch, ctx, ws = gpu
     inp = workload.layer(5, T=2, off=10, H=8, KV=2)
