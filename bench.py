@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 full-attention path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only NAMES] [--copy-calib MB]
 
 Headline line (one JSON object on stdout): decode attention GB/s at 8K KV, on the workload
 "decode_8k_batch32": 32 sequences x (16 query heads, 4 kv heads, head_dim 256), 8192 fp16 KV rows each
@@ -10,7 +10,11 @@ Algorithmic bytes per sequence: K/V read 8192*4*256*2*2 + q, gate, out fp32 (3*1
 (2*4*256*4) + fp16 append (2*4*256*2) = 33,615,872 B; 32 sequences = 1,075,707,904 B per step (> the
 256 MB last-level cache, so the rate is an HBM rate).
 The same line carries the prefill figure (TFLOP/s against the dense fp16 MFMA peak) for "prefill_4k":
-4096 causal rows from an empty cache, 16 query heads, 4 kv heads; FLOPs = 4*H*256*sum_t(t+1).
+4096 causal rows from an empty cache, 16 query heads, 4 kv heads; FLOPs = 4*H*256*sum_t(t+1), and the
+other workloads (ragged decode, verify, short decode, prefill over a cached prefix) under "workloads".
+
+--copy-calib MB runs a plain device copy of MB MiB (three times) before the workloads: its kernel gives the
+bytes-per-count scale of the FETCH_SIZE / WRITE_SIZE counters when the run is profiled.
 """
 import argparse
 import json
@@ -37,12 +41,19 @@ def load_package():
     return mod
 
 
-def decode_bytes(nseq, H, KV, L):
-    per = L * KV * D * 2 * 2 + 3 * H * D * 4 + 2 * KV * D * 4 + 2 * KV * D * 2
-    return nseq * per
+def decode_bytes(H, KV, lens):
+    """Algorithmic bytes of single-token decodes: fp16 K/V rows read, q/gate/out fp32, new K/V fp32 in, fp16 out."""
+    per_seq = 3 * H * D * 4 + 2 * KV * D * 4 + 2 * KV * D * 2
+    return sum(L * KV * D * 2 * 2 for L in lens) + len(lens) * per_seq
 
 
-def prefill_flops(H, T, off):
+def attn_bytes(H, KV, T, off, q_bytes=4):
+    """Algorithmic bytes of a T-row call: cache rows [0, off) read once, q (q_bytes/elem), gate and out fp32,
+    new K/V fp32 in and fp16 out (the new rows are then read from the cache in fp16)."""
+    return (off * KV * D * 2 * 2 + T * H * D * (q_bytes + 4 + 4) + T * KV * D * 2 * (4 + 2) + T * KV * D * 2 * 2)
+
+
+def attn_flops(H, T, off):
     return 4 * H * D * sum(off + t + 1 for t in range(T))
 
 
@@ -51,8 +62,9 @@ def rms(torch, x):
 
 
 def time_steps(torch, fn, steps, warmup):
-    """Runs warmup untimed steps, then `steps` timed ones bracketed by synchronisations; per-step HIP events
-    on the launch stream (torch's current stream) give the average step (kernel) duration."""
+    """Runs `warmup` untimed steps, then `steps` timed ones bracketed by synchronisations. HIP events recorded on
+    the launch stream (torch's current stream, where the library launches) around every step give the average
+    step duration; a step is one library call (one kernel launch unless stated)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -65,55 +77,81 @@ def time_steps(torch, fn, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    total_ms = ev[0].elapsed_time(ev[steps])
-    return total_ms / steps, per, wall
+    return sum(per) / steps, per, wall
 
 
-def bench_decode(torch, ba, ctx, steps, warmup, nseq=32, H=16, KV=4, L=8192):
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0xB0A5A104)
-    dev = "cuda"
-    kc = rms(torch, torch.randn(nseq * L, KV, D, device=dev, generator=g)).half().view(torch.int16)
-    vc = torch.randn(nseq * L, KV, D, device=dev, generator=g).half().view(torch.int16)
-    q = rms(torch, torch.randn(nseq, H, D, device=dev, generator=g))
-    k_new = rms(torch, torch.randn(nseq, KV, D, device=dev, generator=g))
-    v_new = torch.randn(nseq, KV, D, device=dev, generator=g)
-    gate = torch.randn(nseq, H, D, device=dev, generator=g)
-    kv_off = torch.arange(nseq, device=dev, dtype=torch.int64) * L
-    kv_len = torch.full((nseq,), L, device=dev, dtype=torch.int32)
-    out = torch.empty(nseq, H, D, device=dev)
-    ws = ba.Workspace(ctx, dev)
+class Workloads:
+    def __init__(self, torch, ba, ctx):
+        self.torch, self.ba, self.ctx = torch, ba, ctx
+        self.ws = ba.Workspace(ctx, "cuda")
 
-    def step():
-        ba.decode_ragged(ctx, ws, q, kc, vc, kv_off, kv_len, L, out=out, k_new=k_new, v_new=v_new, gate=gate)
+    def _gen(self, seed):
+        g = self.torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        return g
 
-    ms, per, wall = time_steps(torch, step, steps, warmup)
-    nbytes = decode_bytes(nseq, H, KV, L)
-    kernel_ms = sum(per) / len(per)
-    return dict(ms=ms, kernel_ms=kernel_ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9,
-                kernel_gbs=nbytes / (kernel_ms * 1e-3) / 1e9, wall=wall)
+    def decode_batch(self, steps, warmup, nseq=32, H=16, KV=4, lens=None, seed=0xB0A5A104):
+        torch, ba, ctx = self.torch, self.ba, self.ctx
+        g = self._gen(seed)
+        if lens is None:
+            lens = [8192] * nseq
+        rows = sum(lens)
+        kc = rms(torch, torch.randn(rows, KV, D, device="cuda", generator=g)).half().view(torch.int16)
+        vc = torch.randn(rows, KV, D, device="cuda", generator=g).half().view(torch.int16)
+        q = rms(torch, torch.randn(nseq, H, D, device="cuda", generator=g))
+        k_new = rms(torch, torch.randn(nseq, KV, D, device="cuda", generator=g))
+        v_new = torch.randn(nseq, KV, D, device="cuda", generator=g)
+        gate = torch.randn(nseq, H, D, device="cuda", generator=g)
+        offs = [0]
+        for L in lens[:-1]:
+            offs.append(offs[-1] + L)
+        kv_off = torch.tensor(offs, device="cuda", dtype=torch.int64)
+        kv_len = torch.tensor(lens, device="cuda", dtype=torch.int32)
+        out = torch.empty(nseq, H, D, device="cuda")
+        max_len = max(lens)
+
+        def step():
+            ba.decode_ragged(ctx, self.ws, q, kc, vc, kv_off, kv_len, max_len, out=out, k_new=k_new, v_new=v_new,
+                             gate=gate)
+
+        ms, per, wall = time_steps(torch, step, steps, warmup)
+        nbytes = decode_bytes(H, KV, lens)
+        del kc, vc
+        return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
+
+    def attn(self, steps, warmup, H, KV, T, off, kind, seed, q_f16_values=False):
+        torch, ba, ctx = self.torch, self.ba, self.ctx
+        g = self._gen(seed)
+        cap = off + T
+        kc = rms(torch, torch.randn(cap, KV, D, device="cuda", generator=g)).half().view(torch.int16)
+        vc = torch.randn(cap, KV, D, device="cuda", generator=g).half().view(torch.int16)
+        q = rms(torch, torch.randn(T, H, D, device="cuda", generator=g))
+        if q_f16_values:
+            q = q.half().float()
+        k_new = rms(torch, torch.randn(T, KV, D, device="cuda", generator=g))
+        v_new = torch.randn(T, KV, D, device="cuda", generator=g)
+        gate = torch.randn(T, H, D, device="cuda", generator=g)
+        out = torch.empty(T, H, D, device="cuda")
+
+        def step():
+            ba.attention(ctx, self.ws, q, kc, vc, off, out=out, k_new=k_new, v_new=v_new, gate=gate, kind=kind)
+
+        ms, per, wall = time_steps(torch, step, steps, warmup)
+        flops = attn_flops(H, T, off)
+        nbytes = attn_bytes(H, KV, T, off)
+        return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12, bytes=nbytes,
+                    gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
 
-def bench_prefill(torch, ba, ctx, steps, warmup, H=16, KV=4, T=4096, off=0):
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0xB0A5A103)
-    dev = "cuda"
-    cap = off + T
-    kc = torch.zeros(cap, KV, D, device=dev, dtype=torch.int16)
-    vc = torch.zeros(cap, KV, D, device=dev, dtype=torch.int16)
-    q = rms(torch, torch.randn(T, H, D, device=dev, generator=g)).half().float()
-    k_new = rms(torch, torch.randn(T, KV, D, device=dev, generator=g)).half().float()
-    v_new = torch.randn(T, KV, D, device=dev, generator=g).half().float()
-    gate = torch.randn(T, H, D, device=dev, generator=g)
-    out = torch.empty(T, H, D, device=dev)
-    ws = ba.Workspace(ctx, dev)
-
-    def step():
-        ba.attention(ctx, ws, q, kc, vc, off, out=out, k_new=k_new, v_new=v_new, gate=gate, kind=ba.KIND_PREFILL)
-
-    ms, per, wall = time_steps(torch, step, steps, warmup)
-    flops = prefill_flops(H, T, off)
-    return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12, wall=wall)
+def copy_calibration(torch, mib):
+    """A plain device-to-device copy of `mib` MiB, three times (reads and writes mib MiB per launch)."""
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
 
 
 def cpu_baseline(budget_s=10.0, H=16, KV=4, L=8192, nseq=2):
@@ -136,10 +174,13 @@ def cpu_baseline(budget_s=10.0, H=16, KV=4, L=8192, nseq=2):
         oracle.decode_ragged(q, kc, vc, offs, lens, z, nthreads=threads)
         t += time.perf_counter() - t0
         reps += 1
-    nbytes = decode_bytes(nseq, H, KV, L) * reps
+    nbytes = decode_bytes(H, KV, [L] * nseq) * reps
     return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{nseq} of the 32 sequences x {reps} reps ({t:.1f} s): oracle in shader order "
                       f"(oracle/bn_oracle.c, -O2, no fast-math), OpenMP {threads} threads"}
+
+
+ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix")
 
 
 def main():
@@ -148,35 +189,66 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--only", default=",".join(ALL), help="comma-separated workloads to run")
+    ap.add_argument("--copy-calib", type=int, default=0, help="MiB of plain device copy to run first")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the attention path has no cross-GPU exchange); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    only = [w for w in args.only.split(",") if w]
     import torch
     ba = load_package().bonsai_attn
     ctx = ba.Context(0)
-    print(f"bench: decode_8k_batch32 steps={args.steps} warmup={args.warmup}", file=sys.stderr, flush=True)
-    dec = bench_decode(torch, ba, ctx, args.steps, args.warmup)
-    print(f"bench: decode {dec['gbs']:.1f} GB/s ({dec['ms']*1e3:.1f} us/step)", file=sys.stderr, flush=True)
-    pre = None
-    if not args.no_prefill:
-        print("bench: prefill_4k", file=sys.stderr, flush=True)
-        pre = bench_prefill(torch, ba, ctx, max(2, args.steps // 4), max(1, args.warmup // 2))
-        print(f"bench: prefill {pre['tflops']:.1f} TFLOP/s ({pre['ms']:.3f} ms/step)", file=sys.stderr, flush=True)
+    W = Workloads(torch, ba, ctx)
+    log = lambda s: print("bench: " + s, file=sys.stderr, flush=True)
+    if args.copy_calib:
+        log(f"copy calibration {args.copy_calib} MiB x3")
+        copy_calibration(torch, args.copy_calib)
+    K, Wm = args.steps, args.warmup
+    res = {}
+    if "decode_8k_batch32" in only:
+        log(f"decode_8k_batch32 steps={K} warmup={Wm}")
+        res["decode_8k_batch32"] = r = W.decode_batch(K, Wm)
+        log(f"  {r['gbs']:.1f} GB/s ({r['ms'] * 1e3:.1f} us/step)")
+    if "prefill_4k" in only:
+        log("prefill_4k")
+        res["prefill_4k"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
+                                       0xB0A5A103, q_f16_values=True)
+        log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
+    if "ragged_32" in only:
+        import random
+        rng = random.Random(0xB0A5A104)
+        lens = [rng.randint(1024, 32768) for _ in range(32)]
+        log(f"ragged_32 (sum of lengths {sum(lens)})")
+        res["ragged_32"] = r = W.decode_batch(K, Wm, lens=lens, seed=0xB0A5A105)
+        r["sum_len"] = sum(lens)
+        log(f"  {r['gbs']:.1f} GB/s ({r['ms'] * 1e3:.1f} us/step)")
+    if "verify_8" in only:
+        log("verify_8")
+        res["verify_8"] = r = W.attn(K, Wm, 8, 2, 8, 2048, ba.KIND_VERIFY, 0xB0A5A102)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "decode_1k" in only:
+        log("decode_1k")
+        res["decode_1k"] = r = W.attn(K, Wm, 8, 2, 1, 1023, ba.KIND_DECODE, 0xB0A5A100)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "prefill_prefix" in only:
+        log("prefill_prefix")
+        res["prefill_prefix"] = r = W.attn(K, Wm, 8, 2, 256, 512, ba.KIND_PREFILL, 0xB0A5A101)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['tflops']:.2f} TFLOP/s")
     cpu = None
     if not args.no_cpu_baseline:
-        print("bench: cpu baseline", file=sys.stderr, flush=True)
+        log("cpu baseline")
         cpu = cpu_baseline()
+    head = res.get("decode_8k_batch32")
     line = {
         "metric": "attn decode GB/s (%HBM peak) @8K KV; prefill TFLOP/s (%MFMA peak)",
-        "value": round(dec["gbs"], 2),
+        "value": round(head["gbs"], 2) if head else None,
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(dec["ms"], 5),
+        "steps": K,
+        "warmup": Wm,
+        "ms_per_step": round(head["ms"], 5) if head else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -184,16 +256,34 @@ def main():
         "data": "synthetic (seeded: RMS-normalised N(0,1) q/k rows, N(0,1) v and gate logits)",
         "config": {"workload": "decode_8k_batch32", "sequences": 32, "q_heads": 16, "kv_heads": 4,
                    "head_dim": 256, "kv_rows_per_sequence": 8192, "kv_dtype": "fp16", "append": True,
-                   "gate": True, "hbm_peak_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "bn::decode_kernel", "algorithmic_bytes": dec["bytes"]},
+                   "gate": True},
+        "roofline": None,
         "cpu_baseline": cpu,
     }
+    if head:
+        line["roofline"] = {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": "bn::decode_kernel (one launch per step)",
+                            "algorithmic_bytes": head["bytes"]}
+    pre = res.get("prefill_4k")
     if pre:
         line["prefill"] = {"workload": "prefill_4k", "value": round(pre["tflops"], 3), "unit": "TFLOP/s",
                            "ms_per_step": round(pre["ms"], 5), "flops": pre["flops"], "peak": MFMA_F16_PEAK_TFLOPS,
                            "frac": round(pre["tflops"] / MFMA_F16_PEAK_TFLOPS, 5)}
+    others = {}
+    for name in ("ragged_32", "verify_8", "decode_1k", "prefill_prefix"):
+        r = res.get(name)
+        if r:
+            o = {"us_per_step": round(r["ms"] * 1e3, 3), "GB/s": round(r["gbs"], 2),
+                 "hbm_frac": round(r["gbs"] / HBM_PEAK_GBS, 4), "bytes": r["bytes"]}
+            if "tflops" in r:
+                o["TFLOP/s"] = round(r["tflops"], 3)
+                o["mfma_frac"] = round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 5)
+            if "sum_len" in r:
+                o["sum_len"] = r["sum_len"]
+            others[name] = o
+    if others:
+        line["workloads"] = others
     print(json.dumps(line), flush=True)
     ctx.close()
 

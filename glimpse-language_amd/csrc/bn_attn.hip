@@ -23,10 +23,6 @@ thread_local char g_check_err[256];
 
 constexpr int kVerifyMax = 16;     // verify rows handled by the verify kernel (model.rs VMAX = 16)
 constexpr int64_t kMaxRows = 1 << 24;  // positions addressable by one call (int32 key indices)
-// The workspace starts with a fixed block of split counters that every call leaves at zero; partial
-// records always follow it, so no call's partials land on another call's counters, whatever the shapes.
-constexpr int64_t kMaxCounters = 65536;
-constexpr size_t kCounterBytes = kMaxCounters * sizeof(uint32_t);
 
 bn_status set_err(char* buf, bn_status s, const char* fmt, ...) {
     va_list ap;
@@ -56,8 +52,8 @@ int64_t decode_chunk(int64_t max_len, int64_t pairs) {
 
 struct DecodePlan {
     int64_t nseq, KV, max_len, chunk, max_splits;
-    size_t cnt_bytes, part_bytes;
-    size_t total() const { return max_splits > 1 ? cnt_bytes + part_bytes : 0; }
+    size_t part_bytes;
+    size_t total() const { return max_splits > 1 ? part_bytes : 0; }
 };
 
 DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len) {
@@ -67,7 +63,6 @@ DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len) {
     p.max_len = max_len;
     p.chunk = decode_chunk(max_len, nseq * KV);
     p.max_splits = ceil_div(max_len, p.chunk);
-    p.cnt_bytes = kCounterBytes;
     p.part_bytes = (size_t)(nseq * KV * p.max_splits) * bn::DEC_PART * sizeof(float);
     return p;
 }
@@ -106,10 +101,6 @@ bn_status check_attn(const bn_attn_args* a, int kind, char* why) {
         return set_err(why, BN_EINVAL, "bad q pointer or strides");
     if (a->gate && (a->g_ts < 0 || a->g_hs < 0 || ((uintptr_t)a->gate & 3)))
         return set_err(why, BN_EINVAL, "bad gate pointer or strides");
-    DecodePlan p = plan_rows(a);
-    if (p.max_splits > 1 && (int64_t)a->T * a->KV > kMaxCounters)
-        return set_err(why, BN_EINVAL, "T*KV = %lld split rows exceed %lld", (long long)a->T * a->KV,
-                       (long long)kMaxCounters);
     size_t need = bn_attn_workspace_size(a);
     if (need && (!a->ws || a->ws_bytes < need || !aligned16(a->ws)))
         return set_err(why, BN_ENOWS, "workspace needs %zu bytes (16-byte aligned), got %zu", need, a->ws_bytes);
@@ -134,8 +125,6 @@ bn_status check_ragged(const bn_ragged_args* a, char* why) {
     if (a->q_ss < 0 || a->q_hs < 0 || ((uintptr_t)a->q & 3)) return set_err(why, BN_EINVAL, "bad q pointer or strides");
     if (a->gate && (a->g_ss < 0 || a->g_hs < 0 || ((uintptr_t)a->gate & 3)))
         return set_err(why, BN_EINVAL, "bad gate pointer or strides");
-    if ((int64_t)a->nseq * a->KV > kMaxCounters)
-        return set_err(why, BN_EINVAL, "nseq*KV exceeds %lld", (long long)kMaxCounters);
     size_t need = bn_ragged_workspace_size(a);
     if (need && (!a->ws || a->ws_bytes < need || !aligned16(a->ws)))
         return set_err(why, BN_ENOWS, "workspace needs %zu bytes (16-byte aligned), got %zu", need, a->ws_bytes);
@@ -160,16 +149,18 @@ bn_status launch_append(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
 
 bn_status launch_decode(bn_ctx* ctx, hipStream_t st, const bn::DecodeArgs& d, const DecodePlan& p) {
     dim3 grid((unsigned)p.max_splits, (unsigned)p.KV, (unsigned)p.nseq);
-    hipLaunchKernelGGL(bn::decode_kernel, grid, dim3(64), 0, st, d);
-    return launched(ctx, "decode_kernel");
+    hipLaunchKernelGGL(bn::decode_split_kernel, grid, dim3(64), 0, st, d);
+    bn_status s = launched(ctx, "decode_split_kernel");
+    if (s || p.max_splits <= 1) return s;
+    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3((unsigned)p.KV, (unsigned)p.nseq), dim3(256), 0, st, d);
+    return launched(ctx, "decode_combine_kernel");
 }
 
 void bind_workspace(bn::DecodeArgs& d, const DecodePlan& p, void* ws) {
     d.chunk = (int)p.chunk;
     d.max_splits = (int)p.max_splits;
     d.max_len = (int)p.max_len;
-    d.cnt = p.max_splits > 1 ? static_cast<uint32_t*>(ws) : nullptr;
-    d.part = p.max_splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.cnt_bytes) : nullptr;
+    d.part = p.max_splits > 1 ? static_cast<float*>(ws) : nullptr;
 }
 
 // T query rows of one sequence as T single-row decodes over the shared cache (row t sees off+t+1 keys).

@@ -11,9 +11,11 @@
 //   query and the scores are fp32-accurate at no extra MFMA cost.
 //   Softmax: online, in the log2 domain (q pre-scaled by log2 e), fp32.
 //   PV: fp32 FMAs on the VALU; each lane owns 8 dims of every other key and the 4 heads.
-//   Combine: each split writes (m, l, acc[256]) per head to the workspace; the last split to finish
-//   (device-scope counter) merges all splits in split order, applies the gate and writes the output, then
-//   re-arms the counter. The merge order is fixed, so results do not depend on scheduling.
+//   Combine: a sequence that fits one split is finished (divided and gated) by its split. Otherwise each
+//   split writes (m, l, acc[256]) per head to the workspace and decode_combine_kernel, launched next on the
+//   same stream, merges them in split order and gates. The kernel boundary makes the partials visible
+//   across the XCDs' separate L2s; a device-scope fence per block (an L2 write-back plus invalidate on
+//   gfx950) would cost far more. The merge order is fixed, so results do not depend on scheduling.
 //   Append: when k_new/v_new are given, the new row (last key of the sequence) is taken from them, rounded
 //   to fp16, used for the score and the PV product, and stored into the cache by the same split.
 #pragma once
@@ -40,15 +42,13 @@ struct DecodeArgs {
     float* out;          // element seq*o_ss + head*o_hs + d
     int64_t o_ss, o_hs;
     float* part;         // [nseq][KV][max_splits][DEC_PART]
-    uint32_t* cnt;       // [nseq][KV], zero between calls
     int KV, chunk, max_splits, max_len;
 };
 
-__global__ __launch_bounds__(64) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
     __shared__ f4 p_lds[16];   // p[key in tile][head]
     __shared__ f4 al_lds;      // per-head rescale of the running accumulators
     __shared__ f4 ml_lds[2];   // final m, l per head
-    __shared__ int last_lds;
 
     const int s = blockIdx.x, kh = blockIdx.y, seq = blockIdx.z;
     const int lane = threadIdx.x;
@@ -238,48 +238,41 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeArgs a) {
             *reinterpret_cast<f4*>(d + 4) = f4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
         }
     }
-    __threadfence();
-    __syncthreads();
-    uint32_t* cnt = a.cnt + (int64_t)seq * a.KV + kh;
-    if (lane == 0) last_lds = (atomicAdd(cnt, 1u) == (uint32_t)(ns - 1));
-    __syncthreads();
-    if (!last_lds) return;
-    __threadfence();
+}
 
-    // merge the splits in split order: lane = (head lane>>4, dims 16*(lane&15) .. +15)
-    const int h = lane >> 4, d0 = (lane & 15) * 16;
+// Merge of the split partials of one (sequence, kv head): M = max m_s, L = sum l_s 2^(m_s - M),
+// out = (sum acc_s 2^(m_s - M)) / L, in split order (attn_combine.comp:10-20), then the gate.
+// Runs as its own launch after decode_split_kernel, so the partials are visible without device-wide fences.
+// Thread t: head t/64, dims 4*(t%64) .. +3.
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+    const int kh = blockIdx.x, seq = blockIdx.y;
+    const int t = threadIdx.x, h = t >> 6, d0 = (t & 63) * 4;
+    const int L = min(a.kv_len ? a.kv_len[seq] : a.len0 + seq * a.len_step, a.max_len);
+    const int ns = L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
+    if (ns <= 1) return;  // written by the split kernel
     const float* pb = a.part + ((int64_t)seq * a.KV + kh) * a.max_splits * DEC_PART;
     float M = -INFINITY;
     for (int sp = 0; sp < ns; sp++) M = fmaxf(M, pb[(int64_t)sp * DEC_PART + h]);
-    float Ls = 0.0f, o[16];
-#pragma unroll
-    for (int e = 0; e < 16; e++) o[e] = 0.0f;
+    float Ls = 0.0f;
+    f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
     for (int sp = 0; sp < ns; sp++) {
         const float* ps = pb + (int64_t)sp * DEC_PART;
         const float w = exp2f(ps[h] - M);
         Ls = fmaf(ps[4 + h], w, Ls);
-        const f4* av = reinterpret_cast<const f4*>(ps + 8 + h * D + d0);
+        const f4 v = *reinterpret_cast<const f4*>(ps + 8 + h * D + d0);
 #pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            const f4 v = av[q4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) o[q4 * 4 + e] = fmaf(v[e], w, o[q4 * 4 + e]);
-        }
+        for (int e = 0; e < 4; e++) o[e] = fmaf(v[e], w, o[e]);
     }
     const int head = kh * 4 + h;
-    float* op = a.out + seq * a.o_ss + head * a.o_hs + d0;
     const float* z = a.gate ? a.gate + seq * a.g_ss + head * a.g_hs + d0 : nullptr;
+    f4 y;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; q4++) {
-        float y[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            y[e] = o[q4 * 4 + e] / Ls;
-            if (z) y[e] = gate_mul(y[e], z[q4 * 4 + e]);
-        }
-        *reinterpret_cast<f4*>(op + q4 * 4) = f4{y[0], y[1], y[2], y[3]};
+    for (int e = 0; e < 4; e++) {
+        y[e] = o[e] / Ls;
+        if (z) y[e] = gate_mul(y[e], z[e]);
     }
-    if (lane == 0) atomicExch(cnt, 0u);
+    *reinterpret_cast<f4*>(a.out + seq * a.o_ss + head * a.o_hs + d0) = y;
 }
 
 }  // namespace bn

@@ -77,10 +77,9 @@ typedef struct bn_attn_args {
     float* out;         /* [T][H][256] fp32 gated attention output */
     int64_t o_ts, o_hs;
 
-    void* ws;        /* device workspace, >= bn_attn_workspace_size(args) bytes (0 = none needed). Its first
-                        256 KiB hold split counters: zero-fill it once before its first use (bn_workspace_clear);
-                        every call leaves the counters at zero, so one workspace serves calls of any shape.
-                        Calls that overlap in time on one workspace race. */
+    void* ws;        /* device workspace (split partials), >= bn_attn_workspace_size(args) bytes, 16-byte
+                        aligned; NULL when the size is 0. No initialisation is needed and nothing in it
+                        outlives the call. Calls that overlap in time on one workspace race. */
     size_t ws_bytes;
 } bn_attn_args;
 
@@ -122,7 +121,8 @@ size_t bn_ragged_workspace_size(const bn_ragged_args* a);
 bn_status bn_attn_check(const bn_attn_args* a, int kind);
 bn_status bn_ragged_check(const bn_ragged_args* a);
 
-/* Zero-fills a workspace on `stream` with a kernel (no memset node: safe inside graph capture). */
+/* Zero-fills device memory on `stream` with a kernel (no memset node: safe inside graph capture). The
+ * attention calls do not need it; it is there for callers that keep their own scratch next to the workspace. */
 bn_status bn_workspace_clear(bn_ctx* ctx, bn_stream stream, void* ws, size_t bytes);
 
 /* ---- the attention call ------------------------------------------------------------------------- */

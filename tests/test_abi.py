@@ -109,9 +109,8 @@ def test_workspace_sizes(lib):
     r.nseq, r.H, r.KV, r.max_len = 32, 16, 4, 32768
     sz = ba.workspace_size(r)
     assert sz > 0 and sz % 16 == 0
-    # a fixed 256 KiB block of split counters, then partial records of (m[4], l[4], acc[4][256]) floats per
-    # (sequence, kv head, split)
-    assert (sz - 262144) % (4 * (8 + 4 * 256)) == 0
+    # partial records of (m[4], l[4], acc[4][256]) floats per (sequence, kv head, split)
+    assert sz % (4 * (8 + 4 * 256)) == 0
 
 
 def test_ragged_check(lib):
