@@ -37,11 +37,15 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 int64_t ceil_div(int64_t x, int64_t m) { return (x + m - 1) / m; }
 
-// Keys per split for single-token decodes: about 4096 one-wave blocks over the whole launch, at least
-// 64 keys per split and at most 64 splits per (sequence, kv head). Depends only on the shapes, so a
-// given shape always gets the same split structure (and the same bits).
+#ifndef BN_DECODE_TARGET_BLOCKS
+#define BN_DECODE_TARGET_BLOCKS 2048
+#endif
+
+// Keys per split for single-token decodes: about BN_DECODE_TARGET_BLOCKS one-wave blocks over the whole
+// launch, at least 64 keys per split and at most 64 splits per (sequence, kv head). Depends only on the
+// shapes, so a given shape always gets the same split structure (and the same bits).
 int64_t decode_chunk(int64_t max_len, int64_t pairs) {
-    int64_t target = 4096 / (pairs > 0 ? pairs : 1);
+    int64_t target = BN_DECODE_TARGET_BLOCKS / (pairs > 0 ? pairs : 1);
     if (target < 1) target = 1;
     int64_t chunk = round_up(ceil_div(max_len, target), 16);
     if (chunk < 64) chunk = 64;
@@ -152,7 +156,7 @@ bn_status launch_decode(bn_ctx* ctx, hipStream_t st, const bn::DecodeArgs& d, co
     hipLaunchKernelGGL(bn::decode_split_kernel, grid, dim3(64), 0, st, d);
     bn_status s = launched(ctx, "decode_split_kernel");
     if (s || p.max_splits <= 1) return s;
-    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3((unsigned)p.KV, (unsigned)p.nseq), dim3(256), 0, st, d);
+    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3(4, (unsigned)p.KV, (unsigned)p.nseq), dim3(64), 0, st, d);
     return launched(ctx, "decode_combine_kernel");
 }
 

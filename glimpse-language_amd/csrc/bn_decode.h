@@ -141,13 +141,13 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
         const int r = min(jt + c, j1 - 1);
         const uint16_t* p = kb + (int64_t)r * kvd + g * 8;
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) kt[ks] = ld_h8(p + ks * 32);
+        for (int ks = 0; ks < 8; ks++) kt[ks] = ld_h8_nt(p + ks * 32);
     };
     auto load_v = [&](int jt, h8* vt) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const int r = min(jt + 2 * i + pvr, j1 - 1);
-            vt[i] = ld_h8(vb + (int64_t)r * kvd + pvd);
+            vt[i] = ld_h8_nt(vb + (int64_t)r * kvd + pvd);
         }
     };
 
@@ -243,19 +243,21 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
 // Merge of the split partials of one (sequence, kv head): M = max m_s, L = sum l_s 2^(m_s - M),
 // out = (sum acc_s 2^(m_s - M)) / L, in split order (attn_combine.comp:10-20), then the gate.
 // Runs as its own launch after decode_split_kernel, so the partials are visible without device-wide fences.
-// Thread t: head t/64, dims 4*(t%64) .. +3.
-__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
-    const int kh = blockIdx.x, seq = blockIdx.y;
-    const int t = threadIdx.x, h = t >> 6, d0 = (t & 63) * 4;
+// Block = one wave per (head, kv head, sequence); lane: dims 4*lane .. +3.
+__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
+    const int h = blockIdx.x, kh = blockIdx.y, seq = blockIdx.z;
+    const int lane = threadIdx.x, d0 = lane * 4;
     const int L = min(a.kv_len ? a.kv_len[seq] : a.len0 + seq * a.len_step, a.max_len);
     const int ns = L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
     if (ns <= 1) return;  // written by the split kernel
     const float* pb = a.part + ((int64_t)seq * a.KV + kh) * a.max_splits * DEC_PART;
     float M = -INFINITY;
-    for (int sp = 0; sp < ns; sp++) M = fmaxf(M, pb[(int64_t)sp * DEC_PART + h]);
+    for (int sp = lane; sp < ns; sp += 64) M = fmaxf(M, pb[(int64_t)sp * DEC_PART + h]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
     float Ls = 0.0f;
     f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
+#pragma unroll 8
     for (int sp = 0; sp < ns; sp++) {
         const float* ps = pb + (int64_t)sp * DEC_PART;
         const float w = exp2f(ps[h] - M);
