@@ -9,6 +9,7 @@
 #include <cstring>
 
 #include "bn_decode.h"
+#include "bn_flash.h"
 #include "bn_util_kernels.h"
 
 struct bn_ctx {
@@ -71,8 +72,39 @@ DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len) {
     return p;
 }
 
-// Rows handled per launch by the row-wise path (verify / prefill through the decode kernel).
-DecodePlan plan_rows(const bn_attn_args* a) { return plan_decode(a->T, a->KV, (int64_t)a->off + a->T); }
+// A single-row call (T == 1): one sequence of off+1 keys.
+DecodePlan plan_one(const bn_attn_args* a) { return plan_decode(1, a->KV, (int64_t)a->off + 1); }
+
+// T >= 2 rows: q-tiles of 32 tokens; the key range of a q-tile is split only when the q-tiles alone give
+// fewer blocks than CUs (then about 512 blocks of equal key tiles). Depends only on the shapes.
+struct FlashPlan {
+    int64_t ntq, ct, max_splits;
+    size_t acc_bytes, ml_bytes;
+    size_t total() const { return max_splits > 1 ? acc_bytes + ml_bytes : 0; }
+};
+
+FlashPlan plan_flash(int64_t T, int64_t off, int64_t KV) {
+    FlashPlan p;
+    p.ntq = ceil_div(T, bn::FL_BQ);
+    const int64_t max_kt = ceil_div(off + T, bn::FL_BK);
+    if (KV * p.ntq >= 256) {
+        p.ct = max_kt;
+    } else {
+        int64_t iters = 0;
+        for (int64_t qt = 0; qt < p.ntq; qt++) {
+            const int64_t t_last = (qt + 1) * bn::FL_BQ < T ? (qt + 1) * bn::FL_BQ : T;
+            iters += ceil_div(off + t_last, bn::FL_BK);
+        }
+        iters *= KV;
+        p.ct = ceil_div(iters, 512);
+        if (p.ct < 1) p.ct = 1;
+    }
+    p.max_splits = ceil_div(max_kt, p.ct);
+    const int64_t rows = KV * p.ntq * p.max_splits * bn::FL_ROWS;
+    p.acc_bytes = (size_t)rows * bn::D * sizeof(float);
+    p.ml_bytes = (size_t)rows * 2 * sizeof(float);
+    return p;
+}
 
 bn_status check_attn(const bn_attn_args* a, int kind, char* why) {
     if (!a) return set_err(why, BN_EINVAL, "args is NULL");
@@ -87,7 +119,6 @@ bn_status check_attn(const bn_attn_args* a, int kind, char* why) {
         return set_err(why, BN_EINVAL, "off + T = %llu exceeds cap = %u", (unsigned long long)a->off + a->T, a->cap);
     if ((int64_t)a->off + a->T > kMaxRows) return set_err(why, BN_EINVAL, "off + T beyond %lld", (long long)kMaxRows);
     if (a->flags & ~BN_Q_F16) return set_err(why, BN_EINVAL, "unknown flags 0x%x", a->flags);
-    if (a->flags & BN_Q_F16) return set_err(why, BN_EINVAL, "BN_Q_F16 is not supported by this build");
     if (!a->kc || !a->vc) return set_err(why, BN_EINVAL, "kc and vc are required");
     if (!aligned16(a->kc) || !aligned16(a->vc)) return set_err(why, BN_EINVAL, "kc/vc must be 16-byte aligned");
     if ((a->k_new == nullptr) != (a->v_new == nullptr))
@@ -101,8 +132,9 @@ bn_status check_attn(const bn_attn_args* a, int kind, char* why) {
     if (!a->q || !a->out) return set_err(why, BN_EINVAL, "q and out are required");
     if (!aligned16(a->out) || (a->o_ts & 3) || (a->o_hs & 3) || a->o_ts < 0 || a->o_hs < 0)
         return set_err(why, BN_EINVAL, "out must be 16-byte aligned with strides that are multiples of 4 floats");
-    if (a->q_ts < 0 || a->q_hs < 0 || ((uintptr_t)a->q & 3))
-        return set_err(why, BN_EINVAL, "bad q pointer or strides");
+    const int64_t qv = (a->flags & BN_Q_F16) ? 8 : 4;  // elements per 16 bytes
+    if (a->q_ts < 0 || a->q_hs < 0 || !aligned16(a->q) || (a->q_ts % qv) || (a->q_hs % qv))
+        return set_err(why, BN_EINVAL, "q must be 16-byte aligned with strides that are whole 16-byte groups");
     if (a->gate && (a->g_ts < 0 || a->g_hs < 0 || ((uintptr_t)a->gate & 3)))
         return set_err(why, BN_EINVAL, "bad gate pointer or strides");
     size_t need = bn_attn_workspace_size(a);
@@ -167,28 +199,25 @@ void bind_workspace(bn::DecodeArgs& d, const DecodePlan& p, void* ws) {
     d.part = p.max_splits > 1 ? static_cast<float*>(ws) : nullptr;
 }
 
-// T query rows of one sequence as T single-row decodes over the shared cache (row t sees off+t+1 keys).
-bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
-    if (a->T > 65535) return set_err(ctx->err, BN_EINVAL, "T = %u rows exceeds the row-wise launch (65535)", a->T);
-    const bool fused_append = a->T == 1;
-    if (a->k_new && !fused_append) {
-        bn_status s = launch_append(ctx, st, a);
-        if (s) return s;
-    }
-    DecodePlan p = plan_rows(a);
+// One query row: the decode kernel with the append fused (the new row is the last key).
+bn_status run_decode(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    DecodePlan p = plan_one(a);
     bn::DecodeArgs d{};
-    d.q = static_cast<const float*>(a->q);
+    if (a->flags & BN_Q_F16)
+        d.q16 = static_cast<const uint16_t*>(a->q);
+    else
+        d.q = static_cast<const float*>(a->q);
     d.q_ss = a->q_ts;
     d.q_hs = a->q_hs;
-    d.k_new = fused_append ? a->k_new : nullptr;
-    d.v_new = fused_append ? a->v_new : nullptr;
+    d.k_new = a->k_new;
+    d.v_new = a->v_new;
     d.kn_ss = (int64_t)a->KV * bn::D;
     d.kc = a->kc;
     d.vc = a->vc;
     d.row0 = 0;
     d.row_step = 0;
     d.len0 = (int32_t)a->off + 1;
-    d.len_step = 1;
+    d.len_step = 0;
     d.gate = a->gate;
     d.g_ss = a->g_ts;
     d.g_hs = a->g_hs;
@@ -198,6 +227,50 @@ bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     d.KV = (int)a->KV;
     bind_workspace(d, p, a->ws);
     return launch_decode(ctx, st, d, p);
+}
+
+// T >= 2 rows: append, then the MFMA kernel (and the split merge when the key range is split).
+bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    if (a->k_new) {
+        bn_status s = launch_append(ctx, st, a);
+        if (s) return s;
+    }
+    FlashPlan p = plan_flash(a->T, a->off, a->KV);
+    bn::FlashArgs f{};
+    if (a->flags & BN_Q_F16)
+        f.q16 = static_cast<const uint16_t*>(a->q);
+    else
+        f.q = static_cast<const float*>(a->q);
+    f.q_ts = a->q_ts;
+    f.q_hs = a->q_hs;
+    f.kc = a->kc;
+    f.vc = a->vc;
+    f.gate = a->gate;
+    f.g_ts = a->g_ts;
+    f.g_hs = a->g_hs;
+    f.out = a->out;
+    f.o_ts = a->o_ts;
+    f.o_hs = a->o_hs;
+    f.T = (int)a->T;
+    f.off = (int)a->off;
+    f.KV = (int)a->KV;
+    f.ntq = (int)p.ntq;
+    f.ct = (int)p.ct;
+    f.max_splits = (int)p.max_splits;
+    if (p.max_splits > 1) {
+        f.part_acc = static_cast<float*>(a->ws);
+        f.part_ml = reinterpret_cast<float*>(static_cast<char*>(a->ws) + p.acc_bytes);
+    }
+    const int64_t blocks = (int64_t)a->KV * p.ntq * p.max_splits;
+    hipLaunchKernelGGL(bn::flash_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
+    bn_status s = launched(ctx, "flash_kernel");
+    if (s || p.max_splits == 1) return s;
+    hipLaunchKernelGGL(bn::flash_combine_kernel, dim3(a->T, a->H), dim3(64), 0, st, f);
+    return launched(ctx, "flash_combine_kernel");
+}
+
+bn_status run(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    return a->T == 1 ? run_decode(ctx, st, a) : run_flash(ctx, st, a);
 }
 
 }  // namespace
@@ -240,7 +313,7 @@ const char* bn_ctx_last_error(const bn_ctx* ctx) { return ctx ? ctx->err : g_che
 
 size_t bn_attn_workspace_size(const bn_attn_args* a) {
     if (!a || a->KV < 1 || a->T < 1) return 0;
-    return plan_rows(a).total();
+    return a->T == 1 ? plan_one(a).total() : plan_flash(a->T, a->off, a->KV).total();
 }
 
 size_t bn_ragged_workspace_size(const bn_ragged_args* a) {
@@ -276,28 +349,28 @@ bn_status bn_attn_decode(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_attn(a, 1, ctx->err);
     if (s) return s;
-    return run_rows(ctx, (hipStream_t)stream, a);
+    return run(ctx, (hipStream_t)stream, a);
 }
 
 bn_status bn_attn_verify(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_attn(a, 2, ctx->err);
     if (s) return s;
-    return run_rows(ctx, (hipStream_t)stream, a);
+    return run(ctx, (hipStream_t)stream, a);
 }
 
 bn_status bn_attn_prefill(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_attn(a, 3, ctx->err);
     if (s) return s;
-    return run_rows(ctx, (hipStream_t)stream, a);
+    return run(ctx, (hipStream_t)stream, a);
 }
 
 bn_status bn_attn_forward(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_attn(a, 0, ctx->err);
     if (s) return s;
-    return run_rows(ctx, (hipStream_t)stream, a);
+    return run(ctx, (hipStream_t)stream, a);
 }
 
 bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_args* a) {

@@ -26,7 +26,8 @@ namespace bn {
 constexpr int DEC_PART = 8 + 4 * D;  // per (sequence, kv head, split): m[4], l[4], acc[4][256] (floats)
 
 struct DecodeArgs {
-    const float* q;      // element seq*q_ss + head*q_hs + d
+    const float* q;      // element seq*q_ss + head*q_hs + d (fp32) ...
+    const uint16_t* q16; // ... or fp16 bits when non-null
     int64_t q_ss, q_hs;
     const float* k_new;  // element seq*kn_ss + kh*256 + d, or null
     const float* v_new;
@@ -72,15 +73,29 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
     // dims ks*32 + g*8 .. +7.
     h8 qb[8];
     {
-        const float* qr = a.q + seq * a.q_ss + (int64_t)(kh * 4 + (c & 3)) * a.q_hs + g * 8;
+        const int64_t qo = seq * a.q_ss + (int64_t)(kh * 4 + (c & 3)) * a.q_hs + g * 8;
         const bool lo = (c & 4) != 0;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
+            float x[8];
+            if (a.q16) {
+                const h8 v = ld_h8(a.q16 + qo + ks * 32);
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = (float)v[e];
+            } else {
+                const f4 u = *reinterpret_cast<const f4*>(a.q + qo + ks * 32);
+                const f4 v = *reinterpret_cast<const f4*>(a.q + qo + ks * 32 + 4);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[e] = u[e];
+                    x[e + 4] = v[e];
+                }
+            }
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                float x = qr[ks * 32 + e] * LOG2E;
-                _Float16 hi = (_Float16)x;
-                qb[ks][e] = lo ? (_Float16)(x - (float)hi) : hi;
+                const float y = x[e] * LOG2E;
+                const _Float16 hi = (_Float16)y;
+                qb[ks][e] = lo ? (_Float16)(y - (float)hi) : hi;
             }
         }
     }
