@@ -7,14 +7,18 @@
 // Decomposition (this kernel's own):
 //   Block = 4 waves = the 4 query heads of one kv head x 32 consecutive tokens (one q-tile), so every K/V tile
 //   staged in LDS serves 128 query rows. Wave w owns head 4*kh + w; lane l owns token l%32.
-//   K/V tiles of 64 keys are loaded to registers one tile ahead and written to LDS (double buffer): K row-major
-//   [key][256] (+16 B pad per row), V transposed [dim][64 keys] (+16 B pad) with the keys of every 16-group
-//   permuted so that one ds_read_b128 gives a lane the 8 keys its PV operand needs.
+//   K/V tiles of 64 keys go HBM/L2 -> LDS with global_load_lds (no registers, no VALU), double-buffered: the
+//   next tile's copy is in flight while the current one is used. Both tiles are row-major [key][256] in LDS;
+//   the 16-byte chunks of row r sit at slot chunk ^ swz(r), which keeps the K operand reads (16 rows, one
+//   chunk) and the transposed V reads (4 rows x 4 chunks) on distinct LDS banks.
 //   S^T = K Q^T on v_mfma_f32_32x32x16_f16 (A = K from LDS, B = Q in registers, fp16): lane l then holds 16
 //   of the 32 keys of its own query row, so the row max / sum need one cross-half shuffle.
-//   Online softmax in fp32 in the log2 domain (scores scaled by log2(e)/16 after the MFMA). P (fp16) is the
-//   A operand of O = P V straight from the S^T registers; O (32 rows x 256 dims, fp32) stays in registers.
-//   Causal masking only on the tiles that cross the diagonal; tiles past it are not visited.
+//   Online softmax in fp32 in the log2 domain (scores scaled by log2(e)/16 after the MFMA), with the running
+//   max moved only when a row's max grows by more than 2^8 (rare), so O is seldom rescaled.
+//   O = P V: P (fp16) is the A operand straight from the S^T registers (its 16-key steps hold keys
+//   {4h..4h+3, 8+4h..8+4h+3} in lane half h), and the V operand comes from two ds_read_b64_tr_b16 reads of the
+//   row-major V tile that fetch exactly those keys. O (32 rows x 256 dims, fp32) stays in registers.
+//   Causal masking only on tiles that cross the diagonal; tiles past it are not visited.
 //   Longest q-tiles first, each kv head pinned to a fixed set of XCDs so its K/V stay in one XCD's L2.
 //   When the q-tiles alone cannot fill the GPU, the key range of a q-tile is split; each split writes
 //   (m, l, acc) per row and flash_combine_kernel merges them in split order.
@@ -25,10 +29,7 @@ namespace bn {
 
 constexpr int FL_BQ = 32;                      // tokens per q-tile
 constexpr int FL_BK = 64;                      // keys per K/V tile
-constexpr int FL_KS = 264;                     // halves per K row in LDS (256 + 8)
-constexpr int FL_VS = 72;                      // halves per V^T row in LDS (64 + 8)
-constexpr int FL_KBUF = FL_BK * FL_KS;         // halves per K stage (16896)
-constexpr int FL_VBUF = D * FL_VS;             // halves per V stage (18432)
+constexpr int FL_TILE = FL_BK * D;             // halves per K (or V) stage: 32 KB
 constexpr int FL_ROWS = 4 * FL_BQ;             // query rows per block
 
 struct FlashArgs {
@@ -48,15 +49,25 @@ struct FlashArgs {
     int max_splits;
 };
 
-// position of key k (0..15) of a 16-key group inside the V^T row: keys {4h..4h+3, 8+4h..8+4h+3} -> 8h..8h+7
-__device__ __forceinline__ int vperm16(int k) { return ((k & 4) << 1) | ((k & 8) >> 1) | (k & 3); }
+typedef short s4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4v lds_s4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// LDS slot of 16-byte chunk c of tile row r: c ^ swz(r) (stays within the row's 32 chunks)
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 __device__ __forceinline__ h8 lds_h8(const uint16_t* p) { return *reinterpret_cast<const h8*>(p); }
 
+__device__ __forceinline__ h4 lds_tr16(const uint16_t* p) {
+    return __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(p)));
+}
+
+__device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 __global__ __launch_bounds__(256) void flash_kernel(FlashArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][FL_KBUF];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][FL_VBUF];
-    __shared__ f4 bc_lds[4][8];  // per wave: 32 floats broadcast (alpha, then 1/l) in row order
+    __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][FL_TILE];
+    __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][FL_TILE];
+    __shared__ f4 bc_lds[4][8];  // per wave: 32 floats broadcast in row order (alpha, then l)
 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const int h = lane >> 5, r32 = lane & 31;
@@ -114,43 +125,18 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashArgs a) {
         }
     }
 
-    // tile loads (rows clamped to the existing cache rows; clamped rows are masked or never read)
-    h8 kr[8], vr[2][4];
-    auto load_tile = [&](int kt) {
+    // Tile copy: wave w moves tile rows 16w .. 16w+15 of K and of V, two rows (1 KB) per instruction; lane l
+    // of an instruction fills LDS slot l%32 of row (l>>5) with global chunk slot ^ swz(row). Rows past the
+    // cache are clamped to its last row (masked, or never read).
+    auto issue_tile = [&](int kt, int buf) {
         const int j0 = kt * FL_BK;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i, key = c >> 5, dc = c & 31;
-            const int row = min(j0 + key, nk - 1);
-            kr[i] = ld_h8(kb + (int64_t)row * kvd + dc * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int u = tid + 256 * i, kg = u & 15, dg = u >> 4;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = min(j0 + 4 * kg + r, nk - 1);
-                vr[i][r] = ld_h8(vb + (int64_t)row * kvd + dg * 8);
-            }
-        }
-    };
-    auto store_tile = [&](int buf) {
-        uint16_t* ks_ = k_lds[buf];
-        uint16_t* vs_ = v_lds[buf];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i, key = c >> 5, dc = c & 31;
-            *reinterpret_cast<h8*>(ks_ + key * FL_KS + dc * 8) = kr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int u = tid + 256 * i, kg = u & 15, dg = u >> 4;
-            const int pb = 16 * (kg >> 2) + vperm16(4 * (kg & 3));
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                h4 v4 = {vr[i][0][e], vr[i][1][e], vr[i][2][e], vr[i][3][e]};
-                *reinterpret_cast<h4*>(vs_ + (dg * 8 + e) * FL_VS + pb) = v4;
-            }
+            const int rr = 16 * w + 2 * i + (lane >> 5);
+            const int c = (lane & 31) ^ swz(rr);
+            const int64_t g = (int64_t)min(j0 + rr, nk - 1) * kvd + c * 8;
+            __builtin_amdgcn_global_load_lds(kb + g, (lds_void_t*)(&k_lds[buf][(16 * w + 2 * i) * D]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vb + g, (lds_void_t*)(&v_lds[buf][(16 * w + 2 * i) * D]), 16, 0, 0);
         }
     };
 
@@ -163,28 +149,35 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashArgs a) {
     const float sc = QK_SCALE * LOG2E;
     const int qpos = a.off + tq;  // this lane's row sees keys <= qpos
 
-    load_tile(kt0);
-    store_tile(0);
+    // V operand addressing (ds_read_b64_tr_b16): in 16-lane group (h, nh), lane s supplies the address of
+    // 4 halves at row k0 + s/4, dims 32dt + 16nh + 4(s%4); lane i then receives dims 32dt + 16nh + i of
+    // rows k0..k0+3. k0 = 16kk + 8rd + 4h, so the two reads rd = 0, 1 give keys {4h..4h+3, 8+4h..8+4h+3}.
+    const int vs = lane & 15, vnh = (lane >> 4) & 1;
+
+    issue_tile(kt0, 0);
+    wait_vm0();
     __syncthreads();
     for (int kt = kt0; kt < kt1; kt++) {
         const int buf = (kt - kt0) & 1;
         const bool more = kt + 1 < kt1;
-        if (more) load_tile(kt + 1);
+        if (more) issue_tile(kt + 1, buf ^ 1);
         const uint16_t* ks_ = k_lds[buf];
         const uint16_t* vs_ = v_lds[buf];
         const int j0 = kt * FL_BK;
 
-        // S^T: two 32-key halves
+        // S^T: two 32-key halves; lane reads row 32k2 + l%32, chunk 2ks + h
         f16x st[2];
 #pragma unroll
         for (int k2 = 0; k2 < 2; k2++) {
+            const int row = 32 * k2 + r32;
+            const uint16_t* kr = ks_ + row * D;
+            const int sw = swz(row);
 #pragma unroll
             for (int r = 0; r < 16; r++) st[k2][r] = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < 16; ks++)
-                st[k2] = mfma32(lds_h8(ks_ + (32 * k2 + r32) * FL_KS + ks * 16 + 8 * h), qb[ks], st[k2]);
+            for (int ks = 0; ks < 16; ks++) st[k2] = mfma32(lds_h8(kr + (((2 * ks + h) ^ sw) << 3)), qb[ks], st[k2]);
         }
-        // scale, causal mask on diagonal tiles, online softmax (log2 domain)
+        // scale, causal mask on diagonal tiles
         const bool diag = j0 + FL_BK - 1 > a.off + t0;
         float tmax = -INFINITY;
 #pragma unroll
@@ -200,9 +193,27 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashArgs a) {
                 tmax = fmaxf(tmax, x);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = exp2f(m_run - m_use);
+        // Conditional rescale: the running max m_run only moves when some row's tile max exceeds it by more
+        // than 8 (log2 units); otherwise p = 2^(x - m_run) <= 256, still exact-range in fp16, and the final
+        // division by l cancels the common factor. The rescale of O (a VALU pass over its 128 registers) is
+        // then a rare, wave-uniform branch.
+        if (__ballot(tmax > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, tmax);
+            const float alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
+            l_run *= alpha;
+            m_run = m_new;
+            // rows of O register r: 8(r/4) + 4h + r%4 -> alpha through LDS
+            float* bc = reinterpret_cast<float*>(bc_lds[w]);
+            if (h == 0) bc[r32] = alpha;
+            f4 al[4];
+#pragma unroll
+            for (int g = 0; g < 4; g++) al[g] = bc_lds[w][2 * g + h];
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[dt][r] *= al[r >> 2][r & 3];
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
         float psum = 0.0f;
         h8 pa[4];
 #pragma unroll
@@ -213,35 +224,34 @@ __global__ __launch_bounds__(256) void flash_kernel(FlashArgs a) {
                 psum += p;
                 pa[2 * k2 + (r >> 3)][r & 7] = (_Float16)p;
             }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-
-        // rescale O rows by alpha (row of register r: 8(r/4) + 4h + r%4)
-        float* bc = reinterpret_cast<float*>(bc_lds[w]);
-        if (h == 0) bc[r32] = alpha;
-        f4 al[4];
-#pragma unroll
-        for (int g = 0; g < 4; g++) al[g] = bc_lds[w][2 * g + h];
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) o[dt][r] *= al[r >> 2][r & 3];
+        l_run += psum;
 
         // O += P V
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++)
+        for (int kk = 0; kk < 4; kk++) {
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-                o[dt] = mfma32(pa[kk], lds_h8(vs_ + (32 * dt + r32) * FL_VS + 16 * kk + 8 * h), o[dt]);
+            for (int dt = 0; dt < 8; dt++) {
+                const int chunk = 4 * dt + 2 * vnh + ((vs & 3) >> 1);
+                h8 vb8;
+#pragma unroll
+                for (int rd = 0; rd < 2; rd++) {
+                    const int row = 16 * kk + 8 * rd + 4 * h + (vs >> 2);
+                    const h4 x = lds_tr16(vs_ + row * D + ((chunk ^ swz(row)) << 3) + 4 * (vs & 1));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) vb8[4 * rd + e] = x[e];
+                }
+                o[dt] = mfma32(pa[kk], vb8, o[dt]);
+            }
+        }
 
-        if (more) store_tile(buf ^ 1);
-        __syncthreads();
+        wait_vm0();       // next tile has landed in LDS
+        __syncthreads();  // ... for every wave, and every wave is done with this one
     }
 
     // row totals (both lane halves hold the same row)
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     float* bc = reinterpret_cast<float*>(bc_lds[w]);
-    if (h == 0) bc[r32] = a.max_splits == 1 ? l_tot : 0.0f;
+    if (h == 0) bc[r32] = l_tot;
     f4 lv[4];
 #pragma unroll
     for (int g = 0; g < 4; g++) lv[g] = bc_lds[w][2 * g + h];
