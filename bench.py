@@ -143,6 +143,19 @@ class Workloads:
                     gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
 
+def measured_traffic(name):
+    """HBM bytes per step from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ (its
+    `traffic_bytes_per_step:` line), or (None, None) when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_step:"):
+                return int(line.split(":")[1]), "profiles/" + name
+    except OSError:
+        pass
+    return None, None
+
+
 def copy_calibration(torch, mib):
     """A plain device-to-device copy of `mib` MiB, three times (reads and writes mib MiB per launch)."""
     n = mib * (1 << 20) // 4
@@ -261,9 +274,12 @@ def main():
         "cpu_baseline": cpu,
     }
     if head:
+        traffic, src = measured_traffic("decode_8k_batch32_hbm_traffic.md")
         line["roofline"] = {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                            "kernel": "bn::decode_kernel (one launch per step)",
+                            "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                            "traffic_source": src,
+                            "kernel": "bn::decode_split_kernel + bn::decode_combine_kernel (one library call, "
+                                      "timed as a whole)",
                             "algorithmic_bytes": head["bytes"]}
     pre = res.get("prefill_4k")
     if pre:

@@ -1,0 +1,113 @@
+"""Golden vectors (tests/golden/*.npz, written by tests/golden/make_golden.py).
+
+CPU: the oracle still reproduces every stored output bit for bit, and the stored outputs agree with a float64
+brute-force softmax attention. GPU: the HIP path through the C ABI matches the stored outputs to the parity bar
+(max-abs 2e-3, identical projected argmax) and writes the fp16 cache rows exactly.
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import workload
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+FILES = sorted(glob.glob(os.path.join(HERE, "golden", "*.npz")))
+ATTN = [f for f in FILES if not os.path.basename(f).startswith("ragged")]
+RAGGED = [f for f in FILES if os.path.basename(f).startswith("ragged")]
+TOL = 2e-3
+D = 256
+
+
+def load(path):
+    with np.load(path, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def cache_after(g, rows):
+    kc, vc = g["kc"].copy(), g["vc"].copy()
+    for i, r in enumerate(rows):
+        kc[r] = oracle.f32_to_f16(g["k_new"][i])
+        vc[r] = oracle.f32_to_f16(g["v_new"][i])
+    return kc, vc
+
+
+def brute(q, kc, vc, off, gate):
+    kf = oracle.f16_to_f32(kc).astype(np.float64)
+    vf = oracle.f16_to_f32(vc).astype(np.float64)
+    T, H = q.shape[0], q.shape[1]
+    out = np.empty((T, H, D))
+    for t in range(T):
+        n = off + t + 1
+        for h in range(H):
+            s = kf[:n, h // 4] @ q[t, h].astype(np.float64) / 16.0
+            p = np.exp(s - s.max())
+            out[t, h] = (p @ vf[:n, h // 4]) / p.sum()
+    return out if gate is None else out / (1.0 + np.exp(-gate.astype(np.float64)))
+
+
+def test_fixtures_present():
+    assert len(ATTN) >= 4 and len(RAGGED) >= 1
+
+
+@pytest.mark.parametrize("path", ATTN, ids=lambda p: os.path.basename(p)[:-4])
+def test_oracle_reproduces_golden(path):
+    g = load(path)
+    T, off, H, KV = (int(x) for x in g["shape"])
+    kc, vc = cache_after(g, range(off, off + T))
+    out = oracle.attend(g["q"], kc, vc, off, g.get("gate"))
+    assert np.array_equal(out, g["out"])
+    assert np.max(np.abs(g["out"] - brute(g["q"], kc, vc, off, g.get("gate")))) < 2e-6
+
+
+@pytest.mark.parametrize("path", RAGGED, ids=lambda p: os.path.basename(p)[:-4])
+def test_oracle_reproduces_golden_ragged(path):
+    g = load(path)
+    kc, vc = cache_after(g, g["kv_off"] + g["kv_len"] - 1)
+    out = oracle.decode_ragged(g["q"], kc, vc, g["kv_off"], g["kv_len"], g["gate"])
+    assert np.array_equal(out, g["out"])
+
+
+def _parity(out, ref, H):
+    err = float(np.max(np.abs(out - ref)))
+    assert err <= TOL, err
+    R = workload.projection(H)
+    assert np.array_equal(workload.projected_argmax(out, R), workload.projected_argmax(ref, R))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ATTN, ids=lambda p: os.path.basename(p)[:-4])
+def test_hip_matches_golden(gpu, path):
+    torch, ctx, ws = gpu
+    from glimpse_language_amd import bonsai_attn as ba
+    g = load(path)
+    T, off, H, KV = (int(x) for x in g["shape"])
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    kc, vc = t(g["kc"].view(np.int16)), t(g["vc"].view(np.int16))
+    gate = t(g["gate"]) if "gate" in g else None
+    out = ba.attention(ctx, ws, t(g["q"]), kc, vc, off, k_new=t(g["k_new"]), v_new=t(g["v_new"]), gate=gate)
+    torch.cuda.synchronize()
+    _parity(out.cpu().numpy(), g["out"], H)
+    kc_ref, vc_ref = cache_after(g, range(off, off + T))
+    assert np.array_equal(kc.cpu().numpy().view(np.uint16), kc_ref)
+    assert np.array_equal(vc.cpu().numpy().view(np.uint16), vc_ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", RAGGED, ids=lambda p: os.path.basename(p)[:-4])
+def test_hip_matches_golden_ragged(gpu, path):
+    torch, ctx, ws = gpu
+    from glimpse_language_amd import bonsai_attn as ba
+    g = load(path)
+    nseq, H, KV = (int(x) for x in g["shape"])
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    kc, vc = t(g["kc"].view(np.int16)), t(g["vc"].view(np.int16))
+    out = ba.decode_ragged(ctx, ws, t(g["q"]), kc, vc, t(g["kv_off"]), t(g["kv_len"]), int(g["kv_len"].max()),
+                           k_new=t(g["k_new"]), v_new=t(g["v_new"]), gate=t(g["gate"]))
+    torch.cuda.synchronize()
+    _parity(out.cpu().numpy(), g["out"], H)
+    kc_ref, vc_ref = cache_after(g, g["kv_off"] + g["kv_len"] - 1)
+    assert np.array_equal(kc.cpu().numpy().view(np.uint16), kc_ref)
+    assert np.array_equal(vc.cpu().numpy().view(np.uint16), vc_ref)
