@@ -231,14 +231,16 @@ def attention(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=No
               stream=None, q_strides=None, g_strides=None):
     """One attention-layer call: append k_new/v_new at [off, off+T), attend causally, gate.
 
-    q: [T, H, 256] fp32; kc/vc: [cap, KV, 256] fp16 (torch.float16 or int16 view); out: [T, H, 256] fp32.
+    q: [T, H, 256] fp32, or fp16 (passed with BN_Q_F16); kc/vc: [cap, KV, 256] fp16 (torch.float16 or int16
+    view); out: [T, H, 256] fp32.
     """
     import torch
     T, H = q.shape[0], q.shape[1]
     cap, KV = kc.shape[0], kc.shape[1]
     if out is None:
         out = torch.empty((T, H, D), dtype=torch.float32, device=q.device)
-    a = attn_args(T, off, H, KV, cap, q, kc, vc, out, k_new, v_new, gate, None, 0, q_strides, g_strides)
+    flags = BN_Q_F16 if q.dtype == torch.float16 else 0
+    a = attn_args(T, off, H, KV, cap, q, kc, vc, out, k_new, v_new, gate, None, flags, q_strides, g_strides)
     need = workspace_size(a)
     buf = ws.get(need) if ws is not None else None
     a.ws = _ptr(buf)

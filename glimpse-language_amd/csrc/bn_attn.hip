@@ -6,15 +6,21 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "bn_decode.h"
 #include "bn_flash.h"
+#include "bn_flash2.h"
 #include "bn_util_kernels.h"
 
 struct bn_ctx {
     int device;
     int cus;
+    // T >= 64 calls use flash2_kernel when they give at least this many 64-token q-tile blocks (default: never,
+    // until it beats flash_kernel; the environment variable BONSAI_ATTN_FLASH2_MIN_BLOCKS overrides it at
+    // context creation, e.g. 1 to run every T >= 64 call through flash2_kernel in tests)
+    int flash2_min_blocks;
     char err[256];
 };
 
@@ -101,6 +107,30 @@ FlashPlan plan_flash(int64_t T, int64_t off, int64_t KV) {
     }
     p.max_splits = ceil_div(max_kt, p.ct);
     const int64_t rows = KV * p.ntq * p.max_splits * bn::FL_ROWS;
+    p.acc_bytes = (size_t)rows * bn::D * sizeof(float);
+    p.ml_bytes = (size_t)rows * 2 * sizeof(float);
+    return p;
+}
+
+// T >= 64 rows with enough 64-token q-tiles to fill the GPU: flash2_kernel (64 rows per wave). Depends only on
+// the shapes.
+bool use_flash2(int64_t T, int64_t KV, int64_t min_blocks) {
+    return T >= bn::F2_BQ && KV * ceil_div(T, bn::F2_BQ) >= min_blocks;
+}
+
+struct Flash2Plan {
+    int64_t ntq, ct, max_splits;
+    size_t acc_bytes, ml_bytes;
+    size_t total() const { return max_splits > 1 ? acc_bytes + ml_bytes : 0; }
+};
+
+Flash2Plan plan_flash2(int64_t T, int64_t off, int64_t KV) {
+    Flash2Plan p;
+    p.ntq = ceil_div(T, bn::F2_BQ);
+    const int64_t max_kt = ceil_div(off + T, bn::F2_BK);
+    p.ct = max_kt;
+    p.max_splits = 1;
+    const int64_t rows = KV * p.ntq * p.max_splits * bn::F2_ROWS;
     p.acc_bytes = (size_t)rows * bn::D * sizeof(float);
     p.ml_bytes = (size_t)rows * 2 * sizeof(float);
     return p;
@@ -229,12 +259,48 @@ bn_status run_decode(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     return launch_decode(ctx, st, d, p);
 }
 
+bn_status run_flash2(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    Flash2Plan p = plan_flash2(a->T, a->off, a->KV);
+    bn::Flash2Args f{};
+    if (a->flags & BN_Q_F16)
+        f.q16 = static_cast<const uint16_t*>(a->q);
+    else
+        f.q = static_cast<const float*>(a->q);
+    f.q_ts = a->q_ts;
+    f.q_hs = a->q_hs;
+    f.kc = a->kc;
+    f.vc = a->vc;
+    f.gate = a->gate;
+    f.g_ts = a->g_ts;
+    f.g_hs = a->g_hs;
+    f.out = a->out;
+    f.o_ts = a->o_ts;
+    f.o_hs = a->o_hs;
+    f.T = (int)a->T;
+    f.off = (int)a->off;
+    f.KV = (int)a->KV;
+    f.ntq = (int)p.ntq;
+    f.ct = (int)p.ct;
+    f.max_splits = (int)p.max_splits;
+    if (p.max_splits > 1) {
+        f.part_acc = static_cast<float*>(a->ws);
+        f.part_ml = reinterpret_cast<float*>(static_cast<char*>(a->ws) + p.acc_bytes);
+    }
+    const int64_t blocks = (int64_t)a->KV * p.ntq * p.max_splits;
+    hipLaunchKernelGGL(bn::flash2_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
+    bn_status s = launched(ctx, "flash2_kernel");
+    if (s || p.max_splits == 1) return s;
+    hipLaunchKernelGGL(bn::flash2_combine_kernel, dim3(a->T, a->H), dim3(64), 0, st, f);
+    return launched(ctx, "flash2_combine_kernel");
+}
+
 // T >= 2 rows: append, then the MFMA kernel (and the split merge when the key range is split).
 bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     if (a->k_new) {
         bn_status s = launch_append(ctx, st, a);
         if (s) return s;
     }
+    if (use_flash2(a->T, a->KV, ctx->flash2_min_blocks)) return run_flash2(ctx, st, a);
     FlashPlan p = plan_flash(a->T, a->off, a->KV);
     bn::FlashArgs f{};
     if (a->flags & BN_Q_F16)
@@ -302,6 +368,11 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
     if (!c) return BN_EDEVICE;
     c->device = device;
     c->cus = prop.multiProcessorCount;
+    c->flash2_min_blocks = 1 << 30;
+    if (const char* e = getenv("BONSAI_ATTN_FLASH2_MIN_BLOCKS")) {
+        const int v = atoi(e);
+        if (v >= 1) c->flash2_min_blocks = v;
+    }
     c->err[0] = 0;
     *out = c;
     return BN_OK;
@@ -313,7 +384,11 @@ const char* bn_ctx_last_error(const bn_ctx* ctx) { return ctx ? ctx->err : g_che
 
 size_t bn_attn_workspace_size(const bn_attn_args* a) {
     if (!a || a->KV < 1 || a->T < 1) return 0;
-    return a->T == 1 ? plan_one(a).total() : plan_flash(a->T, a->off, a->KV).total();
+    if (a->T == 1) return plan_one(a).total();
+    // the kernel choice for T >= 2 depends on the context, so the size covers both families
+    const size_t f2 = a->T >= (uint32_t)bn::F2_BQ ? plan_flash2(a->T, a->off, a->KV).total() : 0;
+    const size_t f1 = plan_flash(a->T, a->off, a->KV).total();
+    return f1 > f2 ? f1 : f2;
 }
 
 size_t bn_ragged_workspace_size(const bn_ragged_args* a) {

@@ -47,5 +47,9 @@ __device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
 
 // reference gate: a * (1 / (1 + exp(-z)))  (gate_rotate.comp:19-22)
 __device__ __forceinline__ float gate_mul(float a, float z) { return a * (1.0f / (1.0f + expf(-z))); }
+// the same product on v_exp_f32 / v_rcp_f32 (about 2 ulp): for epilogues that gate many rows per lane
+__device__ __forceinline__ float gate_mul_fast(float a, float z) {
+    return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * LOG2E));
+}
 
 }  // namespace bn
