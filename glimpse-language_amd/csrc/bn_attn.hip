@@ -12,6 +12,7 @@
 #include "bn_decode.h"
 #include "bn_flash.h"
 #include "bn_flash2.h"
+#include "bn_prefill.h"
 #include "bn_util_kernels.h"
 
 struct bn_ctx {
@@ -21,6 +22,9 @@ struct bn_ctx {
     // until it beats flash_kernel; the environment variable BONSAI_ATTN_FLASH2_MIN_BLOCKS overrides it at
     // context creation, e.g. 1 to run every T >= 64 call through flash2_kernel in tests)
     int flash2_min_blocks;
+    // T >= 2 calls use prefill_kernel when they give at least this many 32-token q-tile blocks (default: the
+    // CU count; BONSAI_ATTN_PREFILL_MIN_BLOCKS overrides it at context creation, e.g. 1 in tests)
+    int prefill_min_blocks;
     char err[256];
 };
 
@@ -116,6 +120,12 @@ FlashPlan plan_flash(int64_t T, int64_t off, int64_t KV) {
 // the shapes.
 bool use_flash2(int64_t T, int64_t KV, int64_t min_blocks) {
     return T >= bn::F2_BQ && KV * ceil_div(T, bn::F2_BQ) >= min_blocks;
+}
+
+// T >= 2 rows with enough 32-token q-tiles to fill the GPU: prefill_kernel (one block per q-tile, the key range
+// split between the block's two wave groups). Depends only on the shapes and the context's threshold.
+bool use_prefill(int64_t T, int64_t KV, int64_t min_blocks) {
+    return T >= 2 && KV * ceil_div(T, bn::PF_BQ) >= min_blocks;
 }
 
 struct Flash2Plan {
@@ -294,12 +304,38 @@ bn_status run_flash2(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     return launched(ctx, "flash2_combine_kernel");
 }
 
+bn_status run_prefill(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    bn::PrefillArgs f{};
+    if (a->flags & BN_Q_F16)
+        f.q16 = static_cast<const uint16_t*>(a->q);
+    else
+        f.q = static_cast<const float*>(a->q);
+    f.q_ts = a->q_ts;
+    f.q_hs = a->q_hs;
+    f.kc = a->kc;
+    f.vc = a->vc;
+    f.gate = a->gate;
+    f.g_ts = a->g_ts;
+    f.g_hs = a->g_hs;
+    f.out = a->out;
+    f.o_ts = a->o_ts;
+    f.o_hs = a->o_hs;
+    f.T = (int)a->T;
+    f.off = (int)a->off;
+    f.KV = (int)a->KV;
+    f.ntq = (int)ceil_div(a->T, bn::PF_BQ);
+    const int64_t blocks = (int64_t)a->KV * f.ntq;
+    hipLaunchKernelGGL(bn::prefill_kernel, dim3((unsigned)blocks), dim3(512), 0, st, f);
+    return launched(ctx, "prefill_kernel");
+}
+
 // T >= 2 rows: append, then the MFMA kernel (and the split merge when the key range is split).
 bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     if (a->k_new) {
         bn_status s = launch_append(ctx, st, a);
         if (s) return s;
     }
+    if (use_prefill(a->T, a->KV, ctx->prefill_min_blocks)) return run_prefill(ctx, st, a);
     if (use_flash2(a->T, a->KV, ctx->flash2_min_blocks)) return run_flash2(ctx, st, a);
     FlashPlan p = plan_flash(a->T, a->off, a->KV);
     bn::FlashArgs f{};
@@ -369,6 +405,11 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
     c->device = device;
     c->cus = prop.multiProcessorCount;
     c->flash2_min_blocks = 1 << 30;
+    c->prefill_min_blocks = c->cus;
+    if (const char* e = getenv("BONSAI_ATTN_PREFILL_MIN_BLOCKS")) {
+        const int v = atoi(e);
+        if (v >= 1) c->prefill_min_blocks = v;
+    }
     if (const char* e = getenv("BONSAI_ATTN_FLASH2_MIN_BLOCKS")) {
         const int v = atoi(e);
         if (v >= 1) c->flash2_min_blocks = v;

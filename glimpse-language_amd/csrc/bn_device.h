@@ -45,6 +45,16 @@ __device__ __forceinline__ f16x mfma32(h8 a, h8 b, f16x c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// x from lane l and lane l ^ 32 (v_permlane32_swap: no LDS round trip), combined
+__device__ __forceinline__ float max_xhalf(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xhalf(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // reference gate: a * (1 / (1 + exp(-z)))  (gate_rotate.comp:19-22)
 __device__ __forceinline__ float gate_mul(float a, float z) { return a * (1.0f / (1.0f + expf(-z))); }
 // the same product on v_exp_f32 / v_rcp_f32 (about 2 ulp): for epilogues that gate many rows per lane

@@ -1,0 +1,290 @@
+// Causal GQA prefill for long prompts on fp16 MFMA: 8 waves per block, the key range of every q-tile split
+// between two wave groups that merge through LDS.
+//
+// Semantics follow attn_split.comp:9-58 + attn_combine.comp:6-21 + gate_rotate.comp:19-22 of the reference:
+// row t (position off+t) of head h attends to cache rows [0, off+t+1) of kv head h/4; softmax(q.k/16) v,
+// then a * sigmoid(gate). The K/V rows of the call are appended to the cache before this kernel runs.
+//
+// Decomposition (this kernel's own):
+//   A q-tile is 32 consecutive tokens of the 4 query heads of one kv head (128 query rows); one block per
+//   q-tile. The block's 8 waves form two groups of 4 (one wave per query head, 32 rows each). Group 0 attends
+//   to the first half of the q-tile's key tiles, group 1 to the second half, each with its own double-buffered
+//   K/V stages in LDS; at the end the two partial (m, l, O) are merged through LDS in group order. Waves w and
+//   w+4 share a SIMD, so one wave's softmax (VALU) overlaps the other's MFMAs.
+//   Splitting the key range inside the block is what balances the causal triangle: a 4096-token prompt has
+//   exactly as many query rows as 256 CUs x 8 waves x 32 rows hold, so whole q-tiles per CU would leave the
+//   short ones idle half the time; with the split a block's cost is half its key range, and blocks issued
+//   longest first pair up (long + short) on each CU.
+//   K/V tiles of 32 keys are copied HBM/L2 -> LDS by global_load_lds (no VGPRs). Rows p and p+16 of a tile
+//   share one 1 KB copy instruction; the pairs are padded (K: 16 B, V: 64 B per pair) so the K operand reads
+//   (16 rows x 16 B per 16 lanes) and the transposed V reads (4 rows x 64 B per 32 lanes) fall on distinct
+//   banks, and every LDS address is one per-lane base register plus an immediate.
+//   S^T = K Q^T on v_mfma_f32_32x32x16_f16 (A = K from LDS, B = Q^T in registers, fp16). Softmax in fp32, log2
+//   domain; the running max moves only when a row's max grows by more than 2^8, so O is rarely rescaled. The
+//   row sums add the fp16-rounded probabilities (v_dot2_f32_f16), the same values the PV product uses.
+//   O += P V with P straight from the S^T registers (A operand) and V from two ds_read_b64_tr_b16 reads that
+//   fetch exactly the keys those registers hold.
+//   Causal masking only on tiles that cross the diagonal; tiles past it are not visited.
+//   Block order: longest q-tiles first, each kv head pinned to a fixed set of XCDs.
+#pragma once
+#include "bn_device.h"
+
+namespace bn {
+
+constexpr int PF_BQ = 32;                 // tokens per q-tile (rows per wave)
+constexpr int PF_BK = 32;                 // keys per K/V tile
+constexpr int PF_KP = 1040;               // bytes per K row pair (rows p, p+16) in LDS
+constexpr int PF_VP = 1088;               // bytes per V row pair
+constexpr int PF_KB = 16 * PF_KP;         // K tile bytes
+constexpr int PF_VB = 16 * PF_VP;         // V tile bytes
+constexpr int PF_STAGE = PF_KB + PF_VB;   // one K + V stage (34,048 B)
+constexpr int PF_LDS = 4 * PF_STAGE;      // 2 groups x 2 stages (136,192 B)
+constexpr int PF_XSLOT = 16384;           // O exchange per wave at the end: 4 tiles of 32 x 32 fp32
+
+struct PrefillArgs {
+    const float* q;          // element t*q_ts + h*q_hs + d (fp32) ...
+    const uint16_t* q16;     // ... or fp16 bits when non-null
+    int64_t q_ts, q_hs;
+    const uint16_t* kc;      // fp16 [rows][KV][256]
+    const uint16_t* vc;
+    const float* gate;       // element t*g_ts + h*g_hs + d, or null
+    int64_t g_ts, g_hs;
+    float* out;              // element t*o_ts + h*o_hs + d
+    int64_t o_ts, o_hs;
+    int T, off, KV, ntq;
+};
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef short pf_s4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) pf_s4v pf_lds_s4_t;
+typedef __attribute__((address_space(3))) void pf_lds_void_t;
+
+__device__ __forceinline__ h8 pf_lds_h8(const uint8_t* p) { return *reinterpret_cast<const h8*>(p); }
+__device__ __forceinline__ h4 pf_lds_tr(const uint8_t* p) {
+    return __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_s4_t*)(p)));
+}
+__device__ __forceinline__ void pf_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[PF_LDS];
+    __shared__ float ml_lds[2][4][2][32];  // per group, wave: m, l of the wave's 32 rows
+    __shared__ f4 bc_lds[8][16];           // per wave: up to 64 floats broadcast in row order
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = wave >> 2, w = wave & 3;  // wave-uniform
+    const int h = lane >> 5, r32 = lane & 31;
+    const int KV = a.KV, ntq = a.ntq;
+
+    // block -> (kv head, q-tile): longest q-tiles (highest index) first
+    int kh, qt;
+    {
+        const int b = blockIdx.x, nb = KV * ntq;
+        int idx;
+        if (8 % KV == 0 && nb % 8 == 0) {
+            // XCD x (= b % 8) serves kv head x % KV
+            const int xcd = b & 7, reps = 8 / KV;
+            kh = xcd % KV;
+            idx = (b >> 3) * reps + xcd / KV;
+        } else {
+            kh = b % KV;
+            idx = b / KV;
+        }
+        qt = ntq - 1 - idx;
+    }
+    const int t0 = qt * PF_BQ;
+    const int t_last = min(a.T, t0 + PF_BQ) - 1;
+    const int nk = a.off + a.T;                          // cache rows that exist
+    const int nt = (a.off + t_last + PF_BK) / PF_BK;     // key tiles the q-tile attends to
+    const int half = (nt + 1) >> 1;
+    const int j_begin = g ? half : 0, j_end = g ? nt : half;
+    const int64_t kvd = (int64_t)KV * D;
+    const uint16_t* kb = a.kc + (int64_t)kh * D;
+    const uint16_t* vb = a.vc + (int64_t)kh * D;
+    const int head = kh * 4 + w;
+
+    // Q^T operand: lane l holds token t0 + l%32 (clamped), dims 16ks + 8h .. +7, fp16
+    h8 qb[16];
+    {
+        const int tl = min(t0 + r32, a.T - 1);
+        if (a.q16) {
+            const uint16_t* qr = a.q16 + (int64_t)tl * a.q_ts + (int64_t)head * a.q_hs + 8 * h;
+#pragma unroll
+            for (int ks = 0; ks < 16; ks++) qb[ks] = ld_h8(qr + ks * 16);
+        } else {
+            const float* qr = a.q + (int64_t)tl * a.q_ts + (int64_t)head * a.q_hs + 8 * h;
+#pragma unroll
+            for (int ks = 0; ks < 16; ks++) qb[ks] = ld_f32x8_as_h8(qr + ks * 16);
+        }
+    }
+
+    // Tile copy (per group): wave w moves row pairs 4w .. 4w+3 of K and of V; lane l of an instruction loads
+    // row p + 16*(l/32), 16-byte chunk l%32, into LDS pair p at byte 16*l. Rows past the cache are clamped to
+    // its last row (masked).
+    auto issue_tile = [&](int j, int stage) {
+        const int j0 = j * PF_BK;
+        const int lim = nk - 1 - j0;                       // last valid row of this tile
+        const char* kt_base = reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd);  // wave-uniform
+        const char* vt_base = reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd);
+        uint8_t* st = lds + (2 * g + stage) * PF_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = 4 * w + i;
+            const uint32_t go = (uint32_t)(min(p + 16 * h, lim) * (int)kvd + r32 * 8) * 2u;
+            __builtin_amdgcn_global_load_lds(kt_base + go, (pf_lds_void_t*)(st + p * PF_KP), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vt_base + go, (pf_lds_void_t*)(st + PF_KB + p * PF_VP), 16, 0, 0);
+        }
+    };
+
+    f16x o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float sc = QK_SCALE * LOG2E;
+    const int qpos = a.off + t0 + r32;  // this lane's row sees keys <= qpos
+
+    // per-lane LDS bases (the rest of every address is an immediate)
+    const int k_lane = (r32 & 15) * PF_KP + (r32 >> 4) * 512 + h * 16;
+    const int vs = lane & 15, vnh = (lane >> 4) & 1;
+    const int v_lane = PF_KB + (4 * h + (vs >> 2)) * PF_VP + 32 * vnh + 8 * (vs & 3);
+    float* bc = reinterpret_cast<float*>(bc_lds[wave]);
+
+    if (j_begin < j_end) issue_tile(j_begin, 0);
+    pf_wait_vm0();
+    __syncthreads();
+    for (int it = 0; it < half; it++) {
+        const int j = j_begin + it;
+        const int stage = it & 1;
+        if (j + 1 < j_end) issue_tile(j + 1, stage ^ 1);
+        if (j < j_end) {
+            const uint8_t* kl = lds + (2 * g + stage) * PF_STAGE + k_lane;
+            const uint8_t* vl = lds + (2 * g + stage) * PF_STAGE + v_lane;
+            const int j0 = j * PF_BK;
+
+            // S^T: lane reads tile row l%32, chunk 2ks + h
+            f16x s;
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[r] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 16; ks++) s = mfma32(pf_lds_h8(kl + ks * 32), qb[ks], s);
+
+            // causal mask on tiles that cross the diagonal; register r holds key j0 + 8(r/4) + 4h + r%4
+            if (j0 + PF_BK - 1 > a.off + t0) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    s[r] = key <= qpos ? s[r] : -INFINITY;
+                }
+            }
+            float tm = s[0];
+#pragma unroll
+            for (int r = 1; r < 16; r++) tm = fmaxf(tm, s[r]);
+            tm = max_xhalf(tm);
+            const float tmax = tm * sc;  // log2 domain
+            // Conditional rescale: m_run moves only when the row's tile max exceeds it by more than 8 (log2
+            // units); otherwise p = 2^(x - m_run) <= 256 stays well inside fp16 and the final division by l
+            // cancels the common factor. Rows with no key yet (m_run = -inf) have O = 0 and just take the max.
+            float alpha = 1.0f;
+            bool moved = false;
+            if (tmax > m_run + 8.0f) {
+                moved = m_run != -INFINITY;
+                alpha = moved ? __builtin_amdgcn_exp2f(m_run - tmax) : 0.0f;
+                m_run = tmax;
+            }
+            if (__ballot(moved)) {
+                if (h == 0) bc[r32] = alpha;
+                f4 al[4];
+#pragma unroll
+                for (int gg = 0; gg < 4; gg++) al[gg] = bc_lds[wave][2 * gg + h];
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o[dt][r] *= al[r >> 2][r & 3];
+            }
+            l_run *= alpha;
+            const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+            h8 pa[2];
+#pragma unroll
+            for (int r = 0; r < 16; r++) pa[r >> 3][r & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(s[r], sc, -m_use));
+            const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+            for (int k = 0; k < 2; k++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const h2 pp = {pa[k][2 * e], pa[k][2 * e + 1]};
+                    l_run = __builtin_amdgcn_fdot2(pp, one, l_run, false);
+                }
+
+            // O += P V over the 32 keys: two 16-key steps; V operand rows 16kk + 8rd + 4h + (l%16)/4
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) {
+                    const int imm0 = kk * 512 + 64 * dt;
+                    const h4 x0 = pf_lds_tr(vl + imm0);
+                    const h4 x1 = pf_lds_tr(vl + imm0 + 8 * PF_VP);
+                    const h8 vop = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                    o[dt] = mfma32(pa[kk], vop, o[dt]);
+                }
+            }
+        }
+        pf_wait_vm0();    // next tile has landed in LDS
+        __syncthreads();  // ... for every wave, and every wave is done with this one
+    }
+
+    // Merge of the two key-range halves (group order), then 1/l and the gate. Group 0 finishes dims 0..127,
+    // group 1 dims 128..255; each hands the other half of its O over through LDS (the K/V stages are free now).
+    const float l_tot = sum_xhalf(l_run);
+    if (h == 0) {
+        ml_lds[g][w][0][r32] = m_run;
+        ml_lds[g][w][1][r32] = l_tot;
+    }
+    {
+        float* xs = reinterpret_cast<float*>(lds + (4 * g + w) * PF_XSLOT);
+#pragma unroll
+        for (int d = 0; d < 4; d++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) xs[(d * 16 + r) * 64 + lane] = g ? o[d][r] : o[4 + d][r];
+    }
+    __syncthreads();
+    {
+        const float m0 = ml_lds[0][w][0][r32], m1 = ml_lds[1][w][0][r32];
+        const float l0 = ml_lds[0][w][1][r32], l1 = ml_lds[1][w][1][r32];
+        const float M = fmaxf(m0, m1);
+        const float w0 = m0 == -INFINITY ? 0.0f : exp2f(m0 - M);
+        const float w1 = m1 == -INFINITY ? 0.0f : exp2f(m1 - M);
+        const float inv = 1.0f / (l0 * w0 + l1 * w1);
+        // own group's factor first, then the other group's
+        if (h == 0) {
+            bc[r32] = (g ? w1 : w0) * inv;
+            bc[32 + r32] = (g ? w0 : w1) * inv;
+        }
+    }
+    f4 fo[4], fx[4];
+#pragma unroll
+    for (int gg = 0; gg < 4; gg++) {
+        fo[gg] = bc_lds[wave][2 * gg + h];
+        fx[gg] = bc_lds[wave][8 + 2 * gg + h];
+    }
+    const float* xp = reinterpret_cast<const float*>(lds + (4 * (1 - g) + w) * PF_XSLOT);
+    const int dbase = g ? 4 : 0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (t >= a.T) continue;
+        float* op = a.out + (int64_t)t * a.o_ts + (int64_t)head * a.o_hs + r32;
+        const float* zp = a.gate ? a.gate + (int64_t)t * a.g_ts + (int64_t)head * a.g_hs + r32 : nullptr;
+        const float f_own = fo[r >> 2][r & 3], f_oth = fx[r >> 2][r & 3];
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const float own = g ? o[4 + d][r] : o[d][r];
+            float y = own * f_own + xp[(d * 16 + r) * 64 + lane] * f_oth;
+            const int col = 32 * (dbase + d);
+            if (zp) y = gate_mul_fast(y, zp[col]);
+            op[col] = y;
+        }
+    }
+}
+
+}  // namespace bn

@@ -1,0 +1,101 @@
+"""Parity of prefill_kernel (8 waves per block, key range split between two wave groups) with the oracle.
+
+By default the library sends a T >= 2 call to prefill_kernel only when it gives at least as many 32-token q-tile
+blocks as the GPU has CUs (for example the 4096-row prefill); here a second context created with
+BONSAI_ATTN_PREFILL_MIN_BLOCKS=1 sends every T >= 2 call there, so small shapes cover its tails, offsets,
+head counts, the merge of an empty or partly empty second half, and its rescale path.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import workload
+from test_gpu_attn import assert_parity, cache_np, to_dev
+from glimpse_language_amd import bonsai_attn as ba
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def pf(gpu):
+    torch, _, _ = gpu
+    old = os.environ.get("BONSAI_ATTN_PREFILL_MIN_BLOCKS")
+    os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"] = "1"
+    try:
+        ctx = ba.Context(0)
+    finally:
+        if old is None:
+            del os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"]
+        else:
+            os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"] = old
+    ws = ba.Workspace(ctx, "cuda")
+    yield torch, ctx, ws
+    torch.cuda.synchronize()
+    ctx.close()
+
+
+def run_case(pf, inp, q16=False, dev=None, append=True):
+    torch, ctx, ws = pf
+    d = dev or to_dev(torch, inp)
+    q = d["q"].half() if q16 else d["q"]
+    out = ba.attention(ctx, ws, q, d["kc"], d["vc"], inp["off"], k_new=d["k_new"] if append else None,
+                       v_new=d["v_new"] if append else None, gate=d["gate"], kind=ba.KIND_PREFILL)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), d
+
+
+# (T, off, H, KV, gate): single-tile q-tiles, tails, offsets that are not multiples of 32 (rows with no key in
+# the second half), head counts with KV not dividing 8, 1 and 2 key tiles per group
+SHAPES = [(2, 0, 4, 1, True), (31, 0, 8, 2, True), (32, 0, 4, 1, False), (33, 0, 4, 1, True),
+          (50, 20, 8, 2, True), (64, 64, 8, 2, True), (100, 37, 12, 3, True), (130, 500, 16, 4, False),
+          (257, 0, 8, 2, True), (256, 512, 8, 2, True), (96, 1000, 4, 1, True), (3, 2000, 8, 2, True)]
+
+
+@pytest.mark.parametrize("T,off,H,KV,gate", SHAPES)
+def test_prefill_kernel_shapes(pf, T, off, H, KV, gate):
+    inp = workload.layer(6000 + 7 * T + off, T=T, off=off, H=H, KV=KV, gate=gate)
+    out, d = run_case(pf, inp)
+    ref, kc_ref, vc_ref = workload.expected(inp)
+    assert_parity(out, ref, H, f"prefill_kernel T={T} off={off} H={H}")
+    assert np.array_equal(cache_np(d["kc"]), kc_ref)
+    assert np.array_equal(cache_np(d["vc"]), vc_ref)
+    out2, _ = run_case(pf, inp, dev=d, append=False)
+    assert np.array_equal(out, out2), "repeat run not bit-identical"
+
+
+def test_prefill_kernel_fp16_q(pf):
+    inp = workload.layer(6100, T=96, off=40, H=8, KV=2)
+    inp["q"] = inp["q"].astype(np.float16).astype(np.float32)  # values the fp16 path carries exactly
+    out, _ = run_case(pf, inp, q16=True)
+    ref, _, _ = workload.expected(inp)
+    assert_parity(out, ref, 8, "prefill_kernel fp16 q")
+
+
+def test_prefill_kernel_rescale_on_late_dominant_key(pf):
+    """A key far above the earlier scores (log2 growth > 8) moves the running max and rescales O; the row then
+    returns that key's V row. Key 250 sits in the first half of the key range of row 50's q-tile (positions
+    300..369, 12 key tiles), key 340 in the second half."""
+    inp = workload.layer(6200, T=70, off=300, H=4, KV=1, gate=False)
+    kc = inp["kc"]
+    for row, head, j in ((50, 2, 250), (60, 1, 290)):
+        kj = oracle.f16_to_f32(kc[j, 0])
+        inp["q"][row, head] = 8.0 * kj  # score of key j: 8*|k_j|^2/16 = 128 (185 in log2 units)
+    out, _ = run_case(pf, inp)
+    ref, _, vc_ref = workload.expected(inp)
+    assert_parity(out, ref, 4, "prefill_kernel rescale")
+    assert np.max(np.abs(out[50, 2] - oracle.f16_to_f32(vc_ref[250, 0]))) < 2e-3
+    assert np.max(np.abs(out[60, 1] - oracle.f16_to_f32(vc_ref[290, 0]))) < 2e-3
+
+
+def test_prefill_kernel_matches_default_path(pf, gpu):
+    """The two kernel families agree (each is within 2e-3 of the oracle; here they are compared directly)."""
+    torch, ctx1, ws1 = gpu
+    inp = workload.layer(6300, T=160, off=96, H=8, KV=2)
+    out2, _ = run_case(pf, inp)
+    d = to_dev(torch, inp)
+    out1 = ba.attention(ctx1, ws1, d["q"], d["kc"], d["vc"], inp["off"], k_new=d["k_new"], v_new=d["v_new"],
+                        gate=d["gate"], kind=ba.KIND_PREFILL)
+    torch.cuda.synchronize()
+    assert np.max(np.abs(out1.cpu().numpy() - out2)) < 1e-3
