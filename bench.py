@@ -10,7 +10,8 @@ Algorithmic bytes per sequence: K/V read 8192*4*256*2*2 + q, gate, out fp32 (3*1
 (2*4*256*4) + fp16 append (2*4*256*2) = 33,615,872 B; 32 sequences = 1,075,707,904 B per step (> the
 256 MB last-level cache, so the rate is an HBM rate).
 The same line carries the prefill figure (TFLOP/s against the dense fp16 MFMA peak) for "prefill_4k":
-4096 causal rows from an empty cache, 16 query heads, 4 kv heads; FLOPs = 4*H*256*sum_t(t+1), and the
+4096 causal rows from an empty cache, 16 query heads, 4 kv heads, fp16 q (fp32 gate and output, new K/V rows
+fp32 rounded to fp16 by the call); FLOPs = 4*H*256*sum_t(t+1), and the
 other workloads (ragged decode, verify, short decode, prefill over a cached prefix) under "workloads".
 
 --copy-calib MB runs a plain device copy of MB MiB (three times) before the workloads: its kernel gives the
@@ -119,15 +120,15 @@ class Workloads:
         del kc, vc
         return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
-    def attn(self, steps, warmup, H, KV, T, off, kind, seed, q_f16_values=False):
+    def attn(self, steps, warmup, H, KV, T, off, kind, seed, q_f16=False):
         torch, ba, ctx = self.torch, self.ba, self.ctx
         g = self._gen(seed)
         cap = off + T
         kc = rms(torch, torch.randn(cap, KV, D, device="cuda", generator=g)).half().view(torch.int16)
         vc = torch.randn(cap, KV, D, device="cuda", generator=g).half().view(torch.int16)
         q = rms(torch, torch.randn(T, H, D, device="cuda", generator=g))
-        if q_f16_values:
-            q = q.half().float()
+        if q_f16:
+            q = q.half()  # passed as fp16 bits (BN_Q_F16)
         k_new = rms(torch, torch.randn(T, KV, D, device="cuda", generator=g))
         v_new = torch.randn(T, KV, D, device="cuda", generator=g)
         gate = torch.randn(T, H, D, device="cuda", generator=g)
@@ -138,7 +139,7 @@ class Workloads:
 
         ms, per, wall = time_steps(torch, step, steps, warmup)
         flops = attn_flops(H, T, off)
-        nbytes = attn_bytes(H, KV, T, off)
+        nbytes = attn_bytes(H, KV, T, off, q_bytes=2 if q_f16 else 4)
         return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12, bytes=nbytes,
                     gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
@@ -227,7 +228,7 @@ def main():
     if "prefill_4k" in only:
         log("prefill_4k")
         res["prefill_4k"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
-                                       0xB0A5A103, q_f16_values=True)
+                                       0xB0A5A103, q_f16=True)
         log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
     if "ragged_32" in only:
         import random

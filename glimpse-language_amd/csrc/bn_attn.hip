@@ -124,8 +124,11 @@ bool use_flash2(int64_t T, int64_t KV, int64_t min_blocks) {
 
 // T >= 2 rows with enough 32-token q-tiles to fill the GPU: prefill_kernel (one block per q-tile, the key range
 // split between the block's two wave groups). Depends only on the shapes and the context's threshold.
-bool use_prefill(int64_t T, int64_t KV, int64_t min_blocks) {
-    return T >= 2 && KV * ceil_div(T, bn::PF_BQ) >= min_blocks;
+// The kernel reads the gate 16 bytes at a time, so a gate pointer or strides that are not whole 16-byte groups
+// take flash_kernel.
+bool use_prefill(const bn_attn_args* a, int64_t min_blocks) {
+    if (a->gate && (!aligned16(a->gate) || (a->g_ts & 3) || (a->g_hs & 3))) return false;
+    return a->T >= 2 && (int64_t)a->KV * ceil_div(a->T, bn::PF_BQ) >= min_blocks;
 }
 
 struct Flash2Plan {
@@ -335,7 +338,7 @@ bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
         bn_status s = launch_append(ctx, st, a);
         if (s) return s;
     }
-    if (use_prefill(a->T, a->KV, ctx->prefill_min_blocks)) return run_prefill(ctx, st, a);
+    if (use_prefill(a, ctx->prefill_min_blocks)) return run_prefill(ctx, st, a);
     if (use_flash2(a->T, a->KV, ctx->flash2_min_blocks)) return run_flash2(ctx, st, a);
     FlashPlan p = plan_flash(a->T, a->off, a->KV);
     bn::FlashArgs f{};

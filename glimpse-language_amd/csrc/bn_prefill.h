@@ -27,6 +27,8 @@
 //   Causal masking only on tiles that cross the diagonal; tiles past it are not visited.
 //   Block order: longest q-tiles first, each kv head pinned to a fixed set of XCDs.
 #pragma once
+#include <type_traits>
+
 #include "bn_device.h"
 
 namespace bn {
@@ -40,6 +42,7 @@ constexpr int PF_VB = 16 * PF_VP;         // V tile bytes
 constexpr int PF_STAGE = PF_KB + PF_VB;   // one K + V stage (34,048 B)
 constexpr int PF_LDS = 4 * PF_STAGE;      // 2 groups x 2 stages (136,192 B)
 constexpr int PF_XSLOT = 16384;           // O exchange per wave at the end: 4 tiles of 32 x 32 fp32
+constexpr int PF_QP = 528;                // row pitch of the fp16 Q staging rows in LDS
 
 struct PrefillArgs {
     const float* q;          // element t*q_ts + h*q_hs + d (fp32) ...
@@ -102,36 +105,69 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     const uint16_t* vb = a.vc + (int64_t)kh * D;
     const int head = kh * 4 + w;
 
-    // Q^T operand: lane l holds token t0 + l%32 (clamped), dims 16ks + 8h .. +7, fp16
-    h8 qb[16];
-    {
-        const int tl = min(t0 + r32, a.T - 1);
-        if (a.q16) {
-            const uint16_t* qr = a.q16 + (int64_t)tl * a.q_ts + (int64_t)head * a.q_hs + 8 * h;
+    // Q rows of the block (4 heads x 32 tokens) are read with coalesced row loads, rounded to fp16 (nearest
+    // even) and staged in the free second stage of each group (heads 0-1 in group 0's, heads 2-3 in group
+    // 1's), padded rows. Waves w and w+4 share the head, so each row is read from memory once.
+    auto q_stage = [&](int hq) -> uint8_t* { return lds + ((hq >> 1) * 2 + 1) * PF_STAGE + (hq & 1) * 32 * PF_QP; };
+    if (a.q16) {
+        u4 x[8];
 #pragma unroll
-            for (int ks = 0; ks < 16; ks++) qb[ks] = ld_h8(qr + ks * 16);
-        } else {
-            const float* qr = a.q + (int64_t)tl * a.q_ts + (int64_t)head * a.q_hs + 8 * h;
+        for (int i = 0; i < 8; i++) {
+            const int R = 16 * wave + 2 * i + h;  // block row: head R/32, token R%32
+            const int tl = min(t0 + (R & 31), a.T - 1);
+            x[i] = *reinterpret_cast<const u4*>(a.q16 + (int64_t)tl * a.q_ts + (int64_t)(kh * 4 + (R >> 5)) * a.q_hs +
+                                                 8 * r32);
+        }
 #pragma unroll
-            for (int ks = 0; ks < 16; ks++) qb[ks] = ld_f32x8_as_h8(qr + ks * 16);
+        for (int i = 0; i < 8; i++) {
+            const int R = 16 * wave + 2 * i + h;
+            *reinterpret_cast<u4*>(q_stage(R >> 5) + (R & 31) * PF_QP + 16 * r32) = x[i];
+        }
+    } else {
+        f4 x[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int R = 16 * wave + i;
+            const int tl = min(t0 + (R & 31), a.T - 1);
+            x[i] = *reinterpret_cast<const f4*>(a.q + (int64_t)tl * a.q_ts + (int64_t)(kh * 4 + (R >> 5)) * a.q_hs +
+                                                4 * lane);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int R = 16 * wave + i;
+            const h4 y = {(_Float16)x[i][0], (_Float16)x[i][1], (_Float16)x[i][2], (_Float16)x[i][3]};
+            *reinterpret_cast<h4*>(q_stage(R >> 5) + (R & 31) * PF_QP + 8 * lane) = y;
         }
     }
 
     // Tile copy (per group): wave w moves row pairs 4w .. 4w+3 of K and of V; lane l of an instruction loads
-    // row p + 16*(l/32), 16-byte chunk l%32, into LDS pair p at byte 16*l. Rows past the cache are clamped to
-    // its last row (masked).
+    // row p + 16*(l/32), 16-byte chunk l%32, into LDS pair p at byte 16*l. The tile base is wave-uniform and
+    // the lane offset fixed; only a tile that reaches past the cache's last row clamps its rows (masked).
+    const uint32_t lane_go = (uint32_t)(16 * h * (int)kvd + r32 * 8) * 2u;
     auto issue_tile = [&](int j, int stage) {
         const int j0 = j * PF_BK;
-        const int lim = nk - 1 - j0;                       // last valid row of this tile
-        const char* kt_base = reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd);  // wave-uniform
-        const char* vt_base = reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd);
         uint8_t* st = lds + (2 * g + stage) * PF_STAGE;
+        if (j0 + PF_BK <= nk) {
+            const char* kt = reinterpret_cast<const char*>(kb + (int64_t)(j0 + 4 * w) * kvd);
+            const char* vt = reinterpret_cast<const char*>(vb + (int64_t)(j0 + 4 * w) * kvd);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int p = 4 * w + i;
-            const uint32_t go = (uint32_t)(min(p + 16 * h, lim) * (int)kvd + r32 * 8) * 2u;
-            __builtin_amdgcn_global_load_lds(kt_base + go, (pf_lds_void_t*)(st + p * PF_KP), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vt_base + go, (pf_lds_void_t*)(st + PF_KB + p * PF_VP), 16, 0, 0);
+            for (int i = 0; i < 4; i++) {
+                const int p = 4 * w + i;
+                __builtin_amdgcn_global_load_lds(kt + i * kvd * 2 + lane_go, (pf_lds_void_t*)(st + p * PF_KP), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vt + i * kvd * 2 + lane_go, (pf_lds_void_t*)(st + PF_KB + p * PF_VP), 16,
+                                                 0, 0);
+            }
+        } else {
+            const int lim = nk - 1 - j0;  // last valid row of this tile
+            const char* kt = reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd);
+            const char* vt = reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = 4 * w + i;
+                const uint32_t go = (uint32_t)(min(p + 16 * h, lim) * (int)kvd + r32 * 8) * 2u;
+                __builtin_amdgcn_global_load_lds(kt + go, (pf_lds_void_t*)(st + p * PF_KP), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vt + go, (pf_lds_void_t*)(st + PF_KB + p * PF_VP), 16, 0, 0);
+            }
         }
     };
 
@@ -151,8 +187,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     float* bc = reinterpret_cast<float*>(bc_lds[wave]);
 
     if (j_begin < j_end) issue_tile(j_begin, 0);
+    __syncthreads();  // Q rows staged
+    // Q^T operand: lane l holds token t0 + l%32 (clamped), dims 16ks + 8h .. +7, fp16
+    h8 qb[16];
+    {
+        const uint8_t* qr = q_stage(w) + r32 * PF_QP + 16 * h;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) qb[ks] = pf_lds_h8(qr + 32 * ks);
+    }
     pf_wait_vm0();
-    __syncthreads();
+    __syncthreads();  // first K/V tile landed; every wave holds its Q (the staging stage is free again)
     for (int it = 0; it < half; it++) {
         const int j = j_begin + it;
         const int stage = it & 1;
@@ -167,7 +211,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) s[r] = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < 16; ks++) s = mfma32(pf_lds_h8(kl + ks * 32), qb[ks], s);
+            for (int ks = 0; ks < 16; ks++) {
+                s = mfma32(pf_lds_h8(kl + ks * 32), qb[ks], s);
+                // keep up to 6 operand reads ahead of the MFMA that uses them (LDS latency under load)
+                if ((ks & 1) == 1) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // 2 DS reads
+                if ((ks & 1) == 1) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMAs
+            }
 
             // causal mask on tiles that cross the diagonal; register r holds key j0 + 8(r/4) + 4h + r%4
             if (j0 + PF_BK - 1 > a.off + t0) {
@@ -224,7 +273,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                     const int imm0 = kk * 512 + 64 * dt;
                     const h4 x0 = pf_lds_tr(vl + imm0);
                     const h4 x1 = pf_lds_tr(vl + imm0 + 8 * PF_VP);
-                    const h8 vop = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                    const h8 vop = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
                     o[dt] = mfma32(pa[kk], vop, o[dt]);
                 }
             }
@@ -235,56 +284,95 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 
     // Merge of the two key-range halves (group order), then 1/l and the gate. Group 0 finishes dims 0..127,
     // group 1 dims 128..255; each hands the other half of its O over through LDS (the K/V stages are free now).
+    // The gate rows of the finished half are fetched first (coalesced, 16 bytes per lane: lane l covers row
+    // 2i + l/32, dims 4(l%32) .. +3 of the half), so their latency hides behind the merge. The group index is
+    // a compile-time constant inside `finish`, so the half of O that is handed over dies at the exchange.
     const float l_tot = sum_xhalf(l_run);
-    if (h == 0) {
-        ml_lds[g][w][0][r32] = m_run;
-        ml_lds[g][w][1][r32] = l_tot;
-    }
-    {
-        float* xs = reinterpret_cast<float*>(lds + (4 * g + w) * PF_XSLOT);
+    auto finish = [&](auto G) {
+        constexpr int gg_ = decltype(G)::value;
+        constexpr int dh = gg_ ? 128 : 0;      // first dim this wave finishes
+        constexpr int give = gg_ ? 0 : 4;      // O tiles handed to the other group
+        constexpr int keep = gg_ ? 4 : 0;      // O tiles finished here
+        f4 gz[16];
+        if (a.gate) {
+            const float* zp = a.gate + (int64_t)head * a.g_hs + dh + 4 * r32;
 #pragma unroll
-        for (int d = 0; d < 4; d++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) xs[(d * 16 + r) * 64 + lane] = g ? o[d][r] : o[4 + d][r];
-    }
-    __syncthreads();
-    {
-        const float m0 = ml_lds[0][w][0][r32], m1 = ml_lds[1][w][0][r32];
-        const float l0 = ml_lds[0][w][1][r32], l1 = ml_lds[1][w][1][r32];
-        const float M = fmaxf(m0, m1);
-        const float w0 = m0 == -INFINITY ? 0.0f : exp2f(m0 - M);
-        const float w1 = m1 == -INFINITY ? 0.0f : exp2f(m1 - M);
-        const float inv = 1.0f / (l0 * w0 + l1 * w1);
-        // own group's factor first, then the other group's
-        if (h == 0) {
-            bc[r32] = (g ? w1 : w0) * inv;
-            bc[32 + r32] = (g ? w0 : w1) * inv;
+            for (int i = 0; i < 16; i++) {
+                const int t = min(t0 + 2 * i + h, a.T - 1);
+                gz[i] = *reinterpret_cast<const f4*>(zp + (int64_t)t * a.g_ts);
+            }
         }
-    }
-    f4 fo[4], fx[4];
+        if (h == 0) {
+            ml_lds[gg_][w][0][r32] = m_run;
+            ml_lds[gg_][w][1][r32] = l_tot;
+        }
+        {
+            // handed-over half, 16 bytes per lane: element (d, r) at ((4d + r/4) * 64 + lane) * 16 + 4 (r%4)
+            f4* xs = reinterpret_cast<f4*>(lds + (4 * gg_ + w) * PF_XSLOT);
 #pragma unroll
-    for (int gg = 0; gg < 4; gg++) {
-        fo[gg] = bc_lds[wave][2 * gg + h];
-        fx[gg] = bc_lds[wave][8 + 2 * gg + h];
-    }
-    const float* xp = reinterpret_cast<const float*>(lds + (4 * (1 - g) + w) * PF_XSLOT);
-    const int dbase = g ? 4 : 0;
+            for (int d = 0; d < 4; d++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (t >= a.T) continue;
-        float* op = a.out + (int64_t)t * a.o_ts + (int64_t)head * a.o_hs + r32;
-        const float* zp = a.gate ? a.gate + (int64_t)t * a.g_ts + (int64_t)head * a.g_hs + r32 : nullptr;
-        const float f_own = fo[r >> 2][r & 3], f_oth = fx[r >> 2][r & 3];
+                for (int q4 = 0; q4 < 4; q4++) {
+                    f4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = o[give + d][4 * q4 + e];
+                    xs[(4 * d + q4) * 64 + lane] = v;
+                }
+        }
+        __syncthreads();
+        {
+            const float m0 = ml_lds[0][w][0][r32], m1 = ml_lds[1][w][0][r32];
+            const float l0 = ml_lds[0][w][1][r32], l1 = ml_lds[1][w][1][r32];
+            const float M = fmaxf(m0, m1);
+            const float w0 = m0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m0 - M);
+            const float w1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
+            const float inv = 1.0f / (l0 * w0 + l1 * w1);
+            // own group's factor first, then the other group's
+            if (h == 0) {
+                bc[r32] = (gg_ ? w1 : w0) * inv;
+                bc[32 + r32] = (gg_ ? w0 : w1) * inv;
+            }
+        }
+        f4 fo[4], fx[4];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            fo[q4] = bc_lds[wave][2 * q4 + h];
+            fx[q4] = bc_lds[wave][8 + 2 * q4 + h];
+        }
+        // merged rows of the finished half, in the slot this wave read from (only this wave touches it): 32-dim
+        // column block d of the half goes to bytes [4096 d, 4096 (d+1)), the same range its handed-over input
+        // occupied, as [32 rows][32 dims]; then read back 16 bytes per lane (row 2i + l/32, dims 4(l%32) .. +3)
+        // for coalesced stores
+        f4* xr = reinterpret_cast<f4*>(lds + (4 * (1 - gg_) + w) * PF_XSLOT);
+        float* yr = reinterpret_cast<float*>(xr);
 #pragma unroll
         for (int d = 0; d < 4; d++) {
-            const float own = g ? o[4 + d][r] : o[d][r];
-            float y = own * f_own + xp[(d * 16 + r) * 64 + lane] * f_oth;
-            const int col = 32 * (dbase + d);
-            if (zp) y = gate_mul_fast(y, zp[col]);
-            op[col] = y;
+            f4 oth[4];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) oth[q4] = xr[(4 * d + q4) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float y = o[keep + d][r] * fo[r >> 2][r & 3] + oth[r >> 2][r & 3] * fx[r >> 2][r & 3];
+                yr[d * 1024 + (8 * (r >> 2) + 4 * h + (r & 3)) * 32 + r32] = y;
+            }
         }
-    }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int t = t0 + 2 * i + h;
+            f4 y = xr[(r32 >> 3) * 256 + (2 * i + h) * 8 + (r32 & 7)];
+            if (t < a.T) {
+                if (a.gate) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) y[e] = gate_mul_fast(y[e], gz[i][e]);
+                }
+                *reinterpret_cast<f4*>(a.out + (int64_t)t * a.o_ts + (int64_t)head * a.o_hs + dh + 4 * r32) = y;
+            }
+        }
+    };
+    if (g == 0)
+        finish(std::integral_constant<int, 0>{});
+    else
+        finish(std::integral_constant<int, 1>{});
 }
 
 }  // namespace bn
