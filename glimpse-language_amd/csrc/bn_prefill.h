@@ -40,7 +40,6 @@ constexpr int PF_VP = 1088;               // bytes per V row pair
 constexpr int PF_KB = 16 * PF_KP;         // K tile bytes
 constexpr int PF_VB = 16 * PF_VP;         // V tile bytes
 constexpr int PF_STAGE = PF_KB + PF_VB;   // one K + V stage (34,048 B)
-constexpr int PF_LDS = 4 * PF_STAGE;      // 2 groups x 2 stages (136,192 B)
 constexpr int PF_XSLOT = 16384;           // O exchange per wave at the end: 4 tiles of 32 x 32 fp32
 constexpr int PF_QP = 528;                // row pitch of the fp16 Q staging rows in LDS
 
@@ -69,7 +68,10 @@ __device__ __forceinline__ h4 pf_lds_tr(const uint8_t* p) {
 __device__ __forceinline__ void pf_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[PF_LDS];
+    // stage 0 and stage 1 of both groups are separate LDS objects: the compiler then sees that a tile copy into
+    // one stage cannot alias reads of the other, and does not wait for the copy before those reads
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_s0[2 * PF_STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_s1[2 * PF_STAGE];
     __shared__ float ml_lds[2][4][2][32];  // per group, wave: m, l of the wave's 32 rows
     __shared__ f4 bc_lds[8][16];           // per wave: up to 64 floats broadcast in row order
 
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     // Q rows of the block (4 heads x 32 tokens) are read with coalesced row loads, rounded to fp16 (nearest
     // even) and staged in the free second stage of each group (heads 0-1 in group 0's, heads 2-3 in group
     // 1's), padded rows. Waves w and w+4 share the head, so each row is read from memory once.
-    auto q_stage = [&](int hq) -> uint8_t* { return lds + ((hq >> 1) * 2 + 1) * PF_STAGE + (hq & 1) * 32 * PF_QP; };
+    auto q_stage = [&](int hq) -> uint8_t* { return lds_s1 + (hq >> 1) * PF_STAGE + (hq & 1) * 32 * PF_QP; };
     if (a.q16) {
         u4 x[8];
 #pragma unroll
@@ -144,9 +146,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     // row p + 16*(l/32), 16-byte chunk l%32, into LDS pair p at byte 16*l. The tile base is wave-uniform and
     // the lane offset fixed; only a tile that reaches past the cache's last row clamps its rows (masked).
     const uint32_t lane_go = (uint32_t)(16 * h * (int)kvd + r32 * 8) * 2u;
-    auto issue_tile = [&](int j, int stage) {
+    auto issue_tile = [&](int j, uint8_t* st) {
         const int j0 = j * PF_BK;
-        uint8_t* st = lds + (2 * g + stage) * PF_STAGE;
         if (j0 + PF_BK <= nk) {
             const char* kt = reinterpret_cast<const char*>(kb + (int64_t)(j0 + 4 * w) * kvd);
             const char* vt = reinterpret_cast<const char*>(vb + (int64_t)(j0 + 4 * w) * kvd);
@@ -186,7 +187,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     const int v_lane = PF_KB + (4 * h + (vs >> 2)) * PF_VP + 32 * vnh + 8 * (vs & 3);
     float* bc = reinterpret_cast<float*>(bc_lds[wave]);
 
-    if (j_begin < j_end) issue_tile(j_begin, 0);
+    uint8_t* const st0 = lds_s0 + g * PF_STAGE;  // this group's stages
+    uint8_t* const st1 = lds_s1 + g * PF_STAGE;
+    if (j_begin < j_end) issue_tile(j_begin, st0);
     __syncthreads();  // Q rows staged
     // Q^T operand: lane l holds token t0 + l%32 (clamped), dims 16ks + 8h .. +7, fp16
     h8 qb[16];
@@ -197,13 +200,13 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     }
     pf_wait_vm0();
     __syncthreads();  // first K/V tile landed; every wave holds its Q (the staging stage is free again)
-    for (int it = 0; it < half; it++) {
+    // one tile: its K/V are in stage `cur`, the next tile is copied into `nxt` meanwhile
+    auto tile_step = [&](int it, const uint8_t* cur, uint8_t* nxt) {
         const int j = j_begin + it;
-        const int stage = it & 1;
-        if (j + 1 < j_end) issue_tile(j + 1, stage ^ 1);
+        if (j + 1 < j_end) issue_tile(j + 1, nxt);
         if (j < j_end) {
-            const uint8_t* kl = lds + (2 * g + stage) * PF_STAGE + k_lane;
-            const uint8_t* vl = lds + (2 * g + stage) * PF_STAGE + v_lane;
+            const uint8_t* kl = cur + k_lane;
+            const uint8_t* vl = cur + v_lane;
             const int j0 = j * PF_BK;
 
             // S^T: lane reads tile row l%32, chunk 2ks + h
@@ -280,6 +283,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         }
         pf_wait_vm0();    // next tile has landed in LDS
         __syncthreads();  // ... for every wave, and every wave is done with this one
+    };
+    // unrolled by two so every copy and every read names its stage object at compile time
+    for (int it = 0; it < half; it += 2) {
+        tile_step(it, st0, st1);
+        if (it + 1 < half) tile_step(it + 1, st1, st0);
     }
 
     // Merge of the two key-range halves (group order), then 1/l and the gate. Group 0 finishes dims 0..127,
@@ -308,7 +316,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         }
         {
             // handed-over half, 16 bytes per lane: element (d, r) at ((4d + r/4) * 64 + lane) * 16 + 4 (r%4)
-            f4* xs = reinterpret_cast<f4*>(lds + (4 * gg_ + w) * PF_XSLOT);
+            f4* xs = reinterpret_cast<f4*>((gg_ ? lds_s1 : lds_s0) + w * PF_XSLOT);
 #pragma unroll
             for (int d = 0; d < 4; d++)
 #pragma unroll
@@ -343,7 +351,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         // column block d of the half goes to bytes [4096 d, 4096 (d+1)), the same range its handed-over input
         // occupied, as [32 rows][32 dims]; then read back 16 bytes per lane (row 2i + l/32, dims 4(l%32) .. +3)
         // for coalesced stores
-        f4* xr = reinterpret_cast<f4*>(lds + (4 * (1 - gg_) + w) * PF_XSLOT);
+        f4* xr = reinterpret_cast<f4*>((gg_ ? lds_s0 : lds_s1) + w * PF_XSLOT);
         float* yr = reinterpret_cast<float*>(xr);
 #pragma unroll
         for (int d = 0; d < 4; d++) {
