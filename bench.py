@@ -63,22 +63,21 @@ def rms(torch, x):
 
 
 def time_steps(torch, fn, steps, warmup):
-    """Runs `warmup` untimed steps, then `steps` timed ones bracketed by synchronisations. HIP events recorded on
-    the launch stream (torch's current stream, where the library launches) around every step give the average
-    step duration; a step is one library call (one kernel launch unless stated)."""
+    """Runs `warmup` untimed steps, then `steps` timed ones bracketed by synchronisations. Two HIP events recorded
+    on the launch stream (torch's current stream, where the library launches) around the timed steps give the
+    average step duration; a step is one library call."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    ev[0].record()
-    for i in range(steps):
+    start.record()
+    for _ in range(steps):
         fn()
-        ev[i + 1].record()
+    end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    return sum(per) / steps, per, wall
+    return start.elapsed_time(end) / steps, wall
 
 
 class Workloads:
@@ -115,7 +114,7 @@ class Workloads:
             ba.decode_ragged(ctx, self.ws, q, kc, vc, kv_off, kv_len, max_len, out=out, k_new=k_new, v_new=v_new,
                              gate=gate)
 
-        ms, per, wall = time_steps(torch, step, steps, warmup)
+        ms, wall = time_steps(torch, step, steps, warmup)
         nbytes = decode_bytes(H, KV, lens)
         del kc, vc
         return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
@@ -137,7 +136,7 @@ class Workloads:
         def step():
             ba.attention(ctx, self.ws, q, kc, vc, off, out=out, k_new=k_new, v_new=v_new, gate=gate, kind=kind)
 
-        ms, per, wall = time_steps(torch, step, steps, warmup)
+        ms, wall = time_steps(torch, step, steps, warmup)
         flops = attn_flops(H, T, off)
         nbytes = attn_bytes(H, KV, T, off, q_bytes=2 if q_f16 else 4)
         return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12, bytes=nbytes,

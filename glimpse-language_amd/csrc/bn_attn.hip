@@ -25,6 +25,10 @@ struct bn_ctx {
     // T >= 2 calls use prefill_kernel when they give at least this many 32-token q-tile blocks (default: the
     // CU count; BONSAI_ATTN_PREFILL_MIN_BLOCKS overrides it at context creation, e.g. 1 in tests)
     int prefill_min_blocks;
+    // waves per decode split block (1, 2, 4, 8 or 16; BONSAI_ATTN_DECODE_WAVES overrides it at context creation)
+    int decode_waves;
+    // waves a decode launch aims at (256 .. BN_DECODE_MAX_TARGET_WAVES; BONSAI_ATTN_DECODE_TARGET_WAVES)
+    int decode_target_waves;
     char err[256];
 };
 
@@ -45,45 +49,58 @@ bn_status set_err(char* buf, bn_status s, const char* fmt, ...) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 int64_t ceil_div(int64_t x, int64_t m) { return (x + m - 1) / m; }
 
-#ifndef BN_DECODE_TARGET_BLOCKS
-#define BN_DECODE_TARGET_BLOCKS 2048
+#ifndef BN_DECODE_TARGET_WAVES
+#define BN_DECODE_TARGET_WAVES 2048
+#endif
+// the workspace query sizes the partials for this many waves (the largest target a context may use)
+#define BN_DECODE_MAX_TARGET_WAVES 4096
+#ifndef BN_DECODE_WAVES
+#define BN_DECODE_WAVES 2
 #endif
 
-// Keys per split for single-token decodes: about BN_DECODE_TARGET_BLOCKS one-wave blocks over the whole
-// launch, at least 64 keys per split and at most 64 splits per (sequence, kv head). Depends only on the
-// shapes, so a given shape always gets the same split structure (and the same bits).
-int64_t decode_chunk(int64_t max_len, int64_t pairs) {
-    int64_t target = BN_DECODE_TARGET_BLOCKS / (pairs > 0 ? pairs : 1);
-    if (target < 1) target = 1;
-    int64_t chunk = round_up(ceil_div(max_len, target), 16);
-    if (chunk < 64) chunk = 64;
-    int64_t cap64 = round_up(ceil_div(max_len, 64), 16);
-    if (chunk < cap64) chunk = cap64;
-    return chunk;
-}
-
+// Single-token decodes: about `target_waves` waves over the launch in blocks of W waves, i.e.
+// target = target_waves / (W KV) splits per kv head, of equal length over the whole batch (the
+// kernels derive the chunk from the device-side lengths with bn::dec_chunk). A launch is `units` blocks wide
+// per kv head, an upper bound of the splits: sum_i ceil(L_i / chunk) <= sum_i L_i / chunk + nseq <=
+// target + nseq, and no sequence takes more than ceil(max_len / 64) splits. The workspace query has no
+// context, so it sizes the partials for W = 1 and BN_DECODE_MAX_TARGET_WAVES, the most splits a context gives.
 struct DecodePlan {
-    int64_t nseq, KV, max_len, chunk, max_splits;
+    int64_t nseq, KV, max_len, target, units, waves;
+    bool multi;  // some sequence may take more than one split (then the partials need the workspace)
     size_t part_bytes;
-    size_t total() const { return max_splits > 1 ? part_bytes : 0; }
+    size_t total() const { return multi ? part_bytes : 0; }
 };
 
-DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len) {
+DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len, int64_t known_len, int64_t waves,
+                       int64_t target_waves) {
     DecodePlan p;
     p.nseq = nseq;
     p.KV = KV;
     p.max_len = max_len;
-    p.chunk = decode_chunk(max_len, nseq * KV);
-    p.max_splits = ceil_div(max_len, p.chunk);
-    p.part_bytes = (size_t)(nseq * KV * p.max_splits) * bn::DEC_PART * sizeof(float);
+    p.waves = waves;
+    p.target = target_waves / (waves * KV);
+    if (p.target < 1) p.target = 1;
+    if (known_len >= 0) {
+        // one sequence of known length: the exact split count
+        const int64_t chunk = bn::dec_chunk(known_len, (int)p.target, (int)max_len);
+        p.units = known_len > 0 ? ceil_div(known_len, chunk) : 1;
+        p.multi = p.units > 1;
+    } else {
+        p.units = p.target + nseq;
+        const int64_t per_seq = ceil_div(max_len, bn::DEC_MIN_CHUNK);
+        if (nseq * per_seq < p.units) p.units = nseq * per_seq;
+        p.multi = max_len > bn::DEC_MIN_CHUNK;
+    }
+    p.part_bytes = (size_t)(KV * p.units) * bn::DEC_PART * sizeof(float);
     return p;
 }
 
 // A single-row call (T == 1): one sequence of off+1 keys.
-DecodePlan plan_one(const bn_attn_args* a) { return plan_decode(1, a->KV, (int64_t)a->off + 1); }
+DecodePlan plan_one(const bn_attn_args* a, int64_t waves, int64_t target_waves) {
+    return plan_decode(1, a->KV, (int64_t)a->off + 1, (int64_t)a->off + 1, waves, target_waves);
+}
 
 // T >= 2 rows: q-tiles of 32 tokens; the key range of a q-tile is split only when the q-tiles alone give
 // fewer blocks than CUs (then about 512 blocks of equal key tiles). Depends only on the shapes.
@@ -227,24 +244,31 @@ bn_status launch_append(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
 }
 
 bn_status launch_decode(bn_ctx* ctx, hipStream_t st, const bn::DecodeArgs& d, const DecodePlan& p) {
-    dim3 grid((unsigned)p.max_splits, (unsigned)p.KV, (unsigned)p.nseq);
-    hipLaunchKernelGGL(bn::decode_split_kernel, grid, dim3(64), 0, st, d);
+    const dim3 grid((unsigned)p.units, (unsigned)p.KV);
+    switch (p.waves) {
+        case 1: hipLaunchKernelGGL(bn::decode_split_kernel<1>, grid, dim3(64), 0, st, d); break;
+        case 2: hipLaunchKernelGGL(bn::decode_split_kernel<2>, grid, dim3(128), 0, st, d); break;
+        case 4: hipLaunchKernelGGL(bn::decode_split_kernel<4>, grid, dim3(256), 0, st, d); break;
+        case 8: hipLaunchKernelGGL(bn::decode_split_kernel<8>, grid, dim3(512), 0, st, d); break;
+        default: hipLaunchKernelGGL(bn::decode_split_kernel<16>, grid, dim3(1024), 0, st, d); break;
+    }
     bn_status s = launched(ctx, "decode_split_kernel");
-    if (s || p.max_splits <= 1) return s;
-    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3(4, (unsigned)p.KV, (unsigned)p.nseq), dim3(64), 0, st, d);
+    if (s || !p.multi) return s;
+    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3((unsigned)p.nseq, (unsigned)p.KV), dim3(256), 0, st, d);
     return launched(ctx, "decode_combine_kernel");
 }
 
 void bind_workspace(bn::DecodeArgs& d, const DecodePlan& p, void* ws) {
-    d.chunk = (int)p.chunk;
-    d.max_splits = (int)p.max_splits;
+    d.nseq = (int)p.nseq;
     d.max_len = (int)p.max_len;
-    d.part = p.max_splits > 1 ? static_cast<float*>(ws) : nullptr;
+    d.target = (int)p.target;
+    d.units = (int)p.units;
+    d.part = p.multi ? static_cast<float*>(ws) : nullptr;
 }
 
 // One query row: the decode kernel with the append fused (the new row is the last key).
 bn_status run_decode(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
-    DecodePlan p = plan_one(a);
+    DecodePlan p = plan_one(a, ctx->decode_waves, ctx->decode_target_waves);
     bn::DecodeArgs d{};
     if (a->flags & BN_Q_F16)
         d.q16 = static_cast<const uint16_t*>(a->q);
@@ -413,6 +437,16 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
         const int v = atoi(e);
         if (v >= 1) c->prefill_min_blocks = v;
     }
+    c->decode_waves = BN_DECODE_WAVES;
+    if (const char* e = getenv("BONSAI_ATTN_DECODE_WAVES")) {
+        const int v = atoi(e);
+        if (v == 1 || v == 2 || v == 4 || v == 8 || v == 16) c->decode_waves = v;
+    }
+    c->decode_target_waves = BN_DECODE_TARGET_WAVES;
+    if (const char* e = getenv("BONSAI_ATTN_DECODE_TARGET_WAVES")) {
+        const int v = atoi(e);
+        if (v >= 256 && v <= BN_DECODE_MAX_TARGET_WAVES) c->decode_target_waves = v;
+    }
     if (const char* e = getenv("BONSAI_ATTN_FLASH2_MIN_BLOCKS")) {
         const int v = atoi(e);
         if (v >= 1) c->flash2_min_blocks = v;
@@ -428,7 +462,7 @@ const char* bn_ctx_last_error(const bn_ctx* ctx) { return ctx ? ctx->err : g_che
 
 size_t bn_attn_workspace_size(const bn_attn_args* a) {
     if (!a || a->KV < 1 || a->T < 1) return 0;
-    if (a->T == 1) return plan_one(a).total();
+    if (a->T == 1) return plan_one(a, 1, BN_DECODE_MAX_TARGET_WAVES).total();
     // the kernel choice for T >= 2 depends on the context, so the size covers both families
     const size_t f2 = a->T >= (uint32_t)bn::F2_BQ ? plan_flash2(a->T, a->off, a->KV).total() : 0;
     const size_t f1 = plan_flash(a->T, a->off, a->KV).total();
@@ -437,7 +471,7 @@ size_t bn_attn_workspace_size(const bn_attn_args* a) {
 
 size_t bn_ragged_workspace_size(const bn_ragged_args* a) {
     if (!a || a->KV < 1 || a->nseq < 1 || a->max_len < 1) return 0;
-    return plan_decode(a->nseq, a->KV, a->max_len).total();
+    return plan_decode(a->nseq, a->KV, a->max_len, -1, 1, BN_DECODE_MAX_TARGET_WAVES).total();
 }
 
 bn_status bn_attn_check(const bn_attn_args* a, int kind) { return check_attn(a, kind, g_check_err); }
@@ -496,7 +530,7 @@ bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_a
     if (!ctx) return BN_EINVAL;
     bn_status s = check_ragged(a, ctx->err);
     if (s) return s;
-    DecodePlan p = plan_decode(a->nseq, a->KV, a->max_len);
+    DecodePlan p = plan_decode(a->nseq, a->KV, a->max_len, -1, ctx->decode_waves, ctx->decode_target_waves);
     bn::DecodeArgs d{};
     d.q = a->q;
     d.q_ss = a->q_ss;

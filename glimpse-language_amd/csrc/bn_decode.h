@@ -3,8 +3,16 @@
 // Semantics follow attn_split.comp:9-58 + attn_combine.comp:6-21 + gate_rotate.comp:19-22 of the reference
 // (query row of head h attends to cache rows [0, L) of kv head h/4, softmax(q.k / 16), gate a*sigmoid(z));
 // the decomposition is this kernel's own:
-//   grid (split, kv head, sequence) x one wave. A split covers `chunk` consecutive keys of one kv head and
-//   serves the 4 query heads that share it, so every K/V byte is read once.
+//   grid (unit, kv head) x one wave. A split covers `chunk` consecutive keys of one sequence and one kv head
+//   and serves the 4 query heads that share it, so every K/V byte is read once.
+//   Balanced splits: the chunk follows the batch's total length, chunk = ceil(sum_i L_i / target) (rounded up
+//   to 16 keys, at least 64, at most the longest sequence), so a ragged batch gets about `target` equal splits
+//   per kv head however its lengths are spread. Sequence i takes n_i = ceil(L_i / chunk) consecutive units
+//   starting at P_i = sum_{k<i} n_k; every block derives chunk, P and n from the lengths itself (a wave-wide
+//   scan over the length array, which sits in L2), so there is no planning launch and a captured graph can
+//   be replayed with new device-side lengths. sum_i n_i <= target + nseq bounds the launch; units past the
+//   last split exit at once. The split structure is a function of the lengths only, so results are
+//   reproducible bit for bit.
 //   QK^T: v_mfma_f32_16x16x32_f16 computes S^T = K Q^T over 16-key tiles. The A operand is the K tile read
 //   straight from HBM in MFMA layout (lane: key l%16, 8 dims per k-step); the B operand holds the 4 heads'
 //   query rows as an fp16 hi/lo pair (columns h and h+4, repeated in 8..15), so hi + lo carries the fp32
@@ -42,63 +50,144 @@ struct DecodeArgs {
     int64_t g_ss, g_hs;
     float* out;          // element seq*o_ss + head*o_hs + d
     int64_t o_ss, o_hs;
-    float* part;         // [nseq][KV][max_splits][DEC_PART]
-    int KV, chunk, max_splits, max_len;
+    float* part;         // [KV][units][DEC_PART]
+    int KV, nseq, max_len;
+    int target;          // splits aimed at per kv head
+    int units;           // launch width per kv head (>= sum_i n_i)
 };
 
-__global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
-    __shared__ f4 p_lds[16];   // p[key in tile][head]
-    __shared__ f4 al_lds;      // per-head rescale of the running accumulators
-    __shared__ f4 ml_lds[2];   // final m, l per head
+constexpr int DEC_MIN_CHUNK = 64;
 
-    const int s = blockIdx.x, kh = blockIdx.y, seq = blockIdx.z;
-    const int lane = threadIdx.x;
-    // keys of this sequence; device-supplied lengths are clamped to the launch bound
-    const int L = min(a.kv_len ? a.kv_len[seq] : a.len0 + seq * a.len_step, a.max_len);
-    const int64_t row0 = a.kv_off ? a.kv_off[seq] : a.row0 + (int64_t)seq * a.row_step;
-    const int ns = L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
-    if (s >= ns) return;
-    const int j0 = s * a.chunk;
-    const int j1 = min(L, j0 + a.chunk);
-    const bool has_new = a.k_new != nullptr && j1 == L;  // this split owns the appended row L-1
-    const int tl = j0 + (j1 - j0 - 1) / 16 * 16;          // first key of the split's last (maybe partial) tile
+// Keys per split for a batch with `sum_len` keys in total (per kv head); the same on host and device.
+__host__ __device__ inline int dec_chunk(int64_t sum_len, int target, int max_len) {
+    int64_t c = (sum_len + target - 1) / target;
+    c = (c + 15) / 16 * 16;
+    if (c < DEC_MIN_CHUNK) c = DEC_MIN_CHUNK;
+    const int64_t cap = ((int64_t)max_len + 15) / 16 * 16;
+    if (c > cap) c = cap;
+    return (int)c;
+}
+
+// keys of sequence i; device-supplied lengths are clamped to the launch bound
+__device__ __forceinline__ int dec_len(const DecodeArgs& a, int i) {
+    return max(0, min(a.kv_len ? a.kv_len[i] : a.len0 + i * a.len_step, a.max_len));
+}
+__device__ __forceinline__ int64_t dec_row0(const DecodeArgs& a, int i) {
+    return a.kv_off ? a.kv_off[i] : a.row0 + (int64_t)i * a.row_step;
+}
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+__device__ __forceinline__ int64_t wave_sum64(int64_t x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+// The split structure of the batch, as seen from one wave: chunk, and for the sequence found, its first
+// unit P, split count n and length L. Sequences are scanned 64 at a time (one per lane).
+struct DecSplit {
+    int chunk, seq, P, n, L;
+};
+
+// Finds the sequence and split that unit `b` works on (seq = -1 when b is past the last split).
+__device__ DecSplit dec_find_unit(const DecodeArgs& a, int b, int lane) {
+    DecSplit r;
+    const int L0 = lane < a.nseq ? dec_len(a, lane) : 0;  // the first 64 lengths stay in registers
+    int64_t tot = L0;
+    for (int base = 64; base < a.nseq; base += 64) tot += base + lane < a.nseq ? dec_len(a, base + lane) : 0;
+    r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len);
+    r.seq = -1;
+    r.P = r.n = r.L = 0;
+    int prefix = 0;
+    for (int base = 0; base < a.nseq; base += 64) {
+        const int Li = base == 0 ? L0 : (base + lane < a.nseq ? dec_len(a, base + lane) : 0);
+        const int n = (Li + r.chunk - 1) / r.chunk;
+        const int incl = wave_incl_scan(n, lane);
+        const int total = __shfl(incl, 63);
+        if (b < prefix + total) {
+            const uint64_t hit = __ballot(prefix + incl > b);
+            const int f = __builtin_ctzll(hit);
+            r.seq = base + f;
+            r.n = __shfl(n, f);
+            r.P = prefix + __shfl(incl, f) - r.n;
+            r.L = __shfl(Li, f);
+            break;
+        }
+        prefix += total;
+    }
+    return r;
+}
+
+// The units of sequence `seq`: its first unit P and split count n.
+__device__ DecSplit dec_find_seq(const DecodeArgs& a, int seq, int lane) {
+    DecSplit r;
+    const int L0 = lane < a.nseq ? dec_len(a, lane) : 0;
+    int64_t tot = L0;
+    for (int base = 64; base < a.nseq; base += 64) tot += base + lane < a.nseq ? dec_len(a, base + lane) : 0;
+    r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len);
+    r.seq = seq;
+    int prefix = 0;
+    for (int base = 0; base <= seq; base += 64) {
+        const int Li = base == 0 ? L0 : (base + lane < a.nseq ? dec_len(a, base + lane) : 0);
+        const int n = (Li + r.chunk - 1) / r.chunk;
+        const int incl = wave_incl_scan(n, lane);
+        if (seq < base + 64) {
+            const int f = seq - base;
+            r.n = __shfl(n, f);
+            r.P = prefix + __shfl(incl, f) - r.n;
+            r.L = __shfl(Li, f);
+            break;
+        }
+        prefix += __shfl(incl, 63);
+    }
+    return r;
+}
+
+// Wave-local LDS hand-off: the wave's LDS writes are complete and visible to its own lanes afterwards.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// W waves per block. A split's 16-key tiles are dealt to the waves in contiguous runs (wave w: tiles
+// [w nt / W, (w+1) nt / W)); each wave keeps its own online softmax, and the block merges the W partial
+// (m, l, acc) in wave order through LDS. One partial (or the finished output) per block.
+template <int W>
+__global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
+    __shared__ f4 p_lds[W][16];   // per wave: p[key in tile][head]
+    __shared__ f4 al_lds[W];      // per wave: per-head rescale of the running accumulators
+    __shared__ f4 ml_lds[W][2];   // per wave: final m, l per head
+    __shared__ float acc_lds[W > 1 ? W : 1][4 * D];  // per wave: acc[head][dim] (W > 1)
+
+    const int b = blockIdx.x, kh = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int wave = W > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
+    const DecSplit sp = dec_find_unit(a, b, lane);
+    if (sp.seq < 0) return;
+    const int seq = sp.seq, L = sp.L, ns = sp.n, s = b - sp.P;
+    const int64_t row0 = dec_row0(a, seq);
+    const int chunk = sp.chunk;
+    const int sj0 = s * chunk;
+    const int sj1 = min(L, sj0 + chunk);
+    // this wave's keys [j0, j1) (empty for waves without a tile)
+    const int nt = (sj1 - sj0 + 15) >> 4;
+    const int j0 = sj0 + 16 * (wave * nt / W);
+    const int j1 = min(sj1, sj0 + 16 * ((wave + 1) * nt / W));
+    const bool has_new = a.k_new != nullptr && j1 == L && j0 < j1;  // this wave owns the appended row L-1
+    const int tl = j0 + (j1 - j0 - 1) / 16 * 16;          // first key of the wave's last (maybe partial) tile
     const int64_t kvd = (int64_t)a.KV * D;
     const uint16_t* kb = a.kc + (row0 * a.KV + kh) * D;
     const uint16_t* vb = a.vc + (row0 * a.KV + kh) * D;
 
     const int c = lane & 15, g = lane >> 4;       // MFMA column / k-group of this lane
     const int pvr = lane >> 5, pvd = (lane & 31) * 8;  // PV layout: key parity, first dim
-
-    // B operand: Q^T, column c = head (c&3), hi part for (c&4)==0 else lo part, k-step ks covers
-    // dims ks*32 + g*8 .. +7.
-    h8 qb[8];
-    {
-        const int64_t qo = seq * a.q_ss + (int64_t)(kh * 4 + (c & 3)) * a.q_hs + g * 8;
-        const bool lo = (c & 4) != 0;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            float x[8];
-            if (a.q16) {
-                const h8 v = ld_h8(a.q16 + qo + ks * 32);
-#pragma unroll
-                for (int e = 0; e < 8; e++) x[e] = (float)v[e];
-            } else {
-                const f4 u = *reinterpret_cast<const f4*>(a.q + qo + ks * 32);
-                const f4 v = *reinterpret_cast<const f4*>(a.q + qo + ks * 32 + 4);
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    x[e] = u[e];
-                    x[e + 4] = v[e];
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float y = x[e] * LOG2E;
-                const _Float16 hi = (_Float16)y;
-                qb[ks][e] = lo ? (_Float16)(y - (float)hi) : hi;
-            }
-        }
-    }
 
     float m_run = -INFINITY, l_run = 0.0f;
     float acc[4][8];
@@ -107,104 +196,137 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
 
-    auto tile = [&](const h8* kt, const h8* vt, int jt, int jlim) {
-        f4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) sacc = mfma16(kt[ks], qb[ks], sacc);
-        float sc[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float v = (sacc[r] + __shfl_xor(sacc[r], 4)) * QK_SCALE;
-            sc[r] = (jt + 4 * g + r < jlim) ? v : -INFINITY;
-        }
-        float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        tm = fmaxf(tm, __shfl_xor(tm, 16));
-        tm = fmaxf(tm, __shfl_xor(tm, 32));
-        const float m_new = fmaxf(m_run, tm);
-        const float alpha = exp2f(m_run - m_new);
-        float p[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) p[r] = exp2f(sc[r] - m_new);
-        l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-        m_run = m_new;
-        if (c < 4) {
-#pragma unroll
-            for (int r = 0; r < 4; r++) p_lds[4 * g + r][c] = p[r];
-            if (g == 0) al_lds[c] = alpha;
-        }
-        __syncthreads();
-        const f4 al = al_lds;
-#pragma unroll
-        for (int h = 0; h < 4; h++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[h][e] *= al[h];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const f4 pv = p_lds[2 * i + pvr];
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float v = (float)vt[i][e];
-#pragma unroll
-                for (int h = 0; h < 4; h++) acc[h][e] = fmaf(pv[h], v, acc[h][e]);
-            }
-        }
-        __syncthreads();
-    };
-
-    // rows past the split end are clamped to its last row (in bounds; their scores are masked)
-    auto load_k = [&](int jt, h8* kt) {
-        const int r = min(jt + c, j1 - 1);
-        const uint16_t* p = kb + (int64_t)r * kvd + g * 8;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) kt[ks] = ld_h8_nt(p + ks * 32);
-    };
-    auto load_v = [&](int jt, h8* vt) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int r = min(jt + 2 * i + pvr, j1 - 1);
-            vt[i] = ld_h8_nt(vb + (int64_t)r * kvd + pvd);
-        }
-    };
-
-    // full tiles [j0, tl) with the next tile's loads in flight, then the last tile [tl, j1)
-    h8 kt[8], vt[8];
-    load_k(j0, kt);
-    load_v(j0, vt);
-    for (int jt = j0; jt < tl; jt += 16) {
-        h8 kn[8], vn[8];
-        load_k(jt + 16, kn);
-        load_v(jt + 16, vn);
-        tile(kt, vt, jt, j1);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            kt[i] = kn[i];
-            vt[i] = vn[i];
-        }
-    }
-    if (has_new) {
-        // row L-1 of the last tile comes from k_new / v_new (fp16, nearest even) and is stored to the cache,
-        // so a call that appends and one that finds the row cached produce the same bits
-        const int rn = L - 1 - tl;  // tile row of the new key
-        const float* kn = a.k_new + seq * a.kn_ss + kh * D;
-        const float* vn = a.v_new + seq * a.kn_ss + kh * D;
-        uint16_t* kdst = a.kc + ((row0 + L - 1) * a.KV + kh) * D;
-        uint16_t* vdst = a.vc + ((row0 + L - 1) * a.KV + kh) * D;
-        if (c == rn) {
+    if (j0 < j1) {
+        // B operand: Q^T, column c = head (c&3), hi part for (c&4)==0 else lo part, k-step ks covers
+        // dims ks*32 + g*8 .. +7.
+        h8 qb[8];
+        {
+            const int64_t qo = seq * a.q_ss + (int64_t)(kh * 4 + (c & 3)) * a.q_hs + g * 8;
+            const bool lo = (c & 4) != 0;
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
-                kt[ks] = ld_f32x8_as_h8(kn + ks * 32 + g * 8);
-                st_h8(kdst + ks * 32 + g * 8, kt[ks]);
-            }
-        }
+                float x[8];
+                if (a.q16) {
+                    const h8 v = ld_h8(a.q16 + qo + ks * 32);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            if (2 * i + pvr == rn) {
-                vt[i] = ld_f32x8_as_h8(vn + pvd);
-                st_h8(vdst + pvd, vt[i]);
+                    for (int e = 0; e < 8; e++) x[e] = (float)v[e];
+                } else {
+                    const f4 u = *reinterpret_cast<const f4*>(a.q + qo + ks * 32);
+                    const f4 v = *reinterpret_cast<const f4*>(a.q + qo + ks * 32 + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        x[e] = u[e];
+                        x[e + 4] = v[e];
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float y = x[e] * LOG2E;
+                    const _Float16 hi = (_Float16)y;
+                    qb[ks][e] = lo ? (_Float16)(y - (float)hi) : hi;
+                }
             }
         }
+
+        auto tile = [&](const h8* kt, const h8* vt, int jt, int jlim) {
+            f4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) sacc = mfma16(kt[ks], qb[ks], sacc);
+            float sc[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float v = (sacc[r] + __shfl_xor(sacc[r], 4)) * QK_SCALE;
+                sc[r] = (jt + 4 * g + r < jlim) ? v : -INFINITY;
+            }
+            float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            tm = fmaxf(tm, __shfl_xor(tm, 16));
+            tm = fmaxf(tm, __shfl_xor(tm, 32));
+            const float m_new = fmaxf(m_run, tm);
+            const float alpha = exp2f(m_run - m_new);
+            float p[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) p[r] = exp2f(sc[r] - m_new);
+            l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+            m_run = m_new;
+            if (c < 4) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) p_lds[wave][4 * g + r][c] = p[r];
+                if (g == 0) al_lds[wave][c] = alpha;
+            }
+            wave_lds_sync();
+            const f4 al = al_lds[wave];
+#pragma unroll
+            for (int h = 0; h < 4; h++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[h][e] *= al[h];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const f4 pv = p_lds[wave][2 * i + pvr];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float v = (float)vt[i][e];
+#pragma unroll
+                    for (int h = 0; h < 4; h++) acc[h][e] = fmaf(pv[h], v, acc[h][e]);
+                }
+            }
+            wave_lds_sync();
+        };
+
+        // rows past the wave's end are clamped to its last row (in bounds; their scores are masked)
+        auto load_k = [&](int jt, h8* kt) {
+            const int r = min(jt + c, j1 - 1);
+            const uint16_t* p = kb + (int64_t)r * kvd + g * 8;
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) kt[ks] = ld_h8_nt(p + ks * 32);
+        };
+        auto load_v = [&](int jt, h8* vt) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int r = min(jt + 2 * i + pvr, j1 - 1);
+                vt[i] = ld_h8_nt(vb + (int64_t)r * kvd + pvd);
+            }
+        };
+
+        // full tiles [j0, tl) with the next tile's loads in flight, then the last tile [tl, j1)
+        h8 kt[8], vt[8];
+        load_k(j0, kt);
+        load_v(j0, vt);
+        for (int jt = j0; jt < tl; jt += 16) {
+            h8 kn[8], vn[8];
+            load_k(jt + 16, kn);
+            load_v(jt + 16, vn);
+            tile(kt, vt, jt, j1);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                kt[i] = kn[i];
+                vt[i] = vn[i];
+            }
+        }
+        if (has_new) {
+            // row L-1 of the last tile comes from k_new / v_new (fp16, nearest even) and is stored to the
+            // cache, so a call that appends and one that finds the row cached produce the same bits
+            const int rn = L - 1 - tl;  // tile row of the new key
+            const float* kn = a.k_new + seq * a.kn_ss + kh * D;
+            const float* vn = a.v_new + seq * a.kn_ss + kh * D;
+            uint16_t* kdst = a.kc + ((row0 + L - 1) * a.KV + kh) * D;
+            uint16_t* vdst = a.vc + ((row0 + L - 1) * a.KV + kh) * D;
+            if (c == rn) {
+#pragma unroll
+                for (int ks = 0; ks < 8; ks++) {
+                    kt[ks] = ld_f32x8_as_h8(kn + ks * 32 + g * 8);
+                    st_h8(kdst + ks * 32 + g * 8, kt[ks]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (2 * i + pvr == rn) {
+                    vt[i] = ld_f32x8_as_h8(vn + pvd);
+                    st_h8(vdst + pvd, vt[i]);
+                }
+            }
+        }
+        tile(kt, vt, tl, j1);
     }
-    tile(kt, vt, tl, j1);
 
     // totals over the lanes holding the same head / dims
     float l_tot = l_run + __shfl_xor(l_run, 16);
@@ -214,80 +336,161 @@ __global__ __launch_bounds__(64) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[h][e] += __shfl_xor(acc[h][e], 32);
     if (lane < 4) {
-        ml_lds[0][lane] = m_run;
-        ml_lds[1][lane] = l_tot;
+        ml_lds[wave][0][lane] = m_run;
+        ml_lds[wave][1][lane] = l_tot;
     }
-    __syncthreads();
 
-    if (ns == 1) {
+    if constexpr (W == 1) {
+        wave_lds_sync();
+        if (ns == 1) {
+            if (lane < 32) {
+                const f4 lsum = ml_lds[0][1];
+#pragma unroll
+                for (int h = 0; h < 4; h++) {
+                    const int head = kh * 4 + h;
+                    float* o = a.out + seq * a.o_ss + head * a.o_hs + pvd;
+                    const float* z = a.gate ? a.gate + seq * a.g_ss + head * a.g_hs + pvd : nullptr;
+                    float y[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        y[e] = acc[h][e] / lsum[h];
+                        if (z) y[e] = gate_mul(y[e], z[e]);
+                    }
+                    *reinterpret_cast<f4*>(o) = f4{y[0], y[1], y[2], y[3]};
+                    *reinterpret_cast<f4*>(o + 4) = f4{y[4], y[5], y[6], y[7]};
+                }
+            }
+            return;
+        }
+        float* pp = a.part + ((int64_t)kh * a.units + b) * DEC_PART;
+        if (lane < 4) {
+            pp[lane] = ml_lds[0][0][lane];
+            pp[4 + lane] = ml_lds[0][1][lane];
+        }
         if (lane < 32) {
-            const f4 lsum = ml_lds[1];
 #pragma unroll
             for (int h = 0; h < 4; h++) {
-                const int head = kh * 4 + h;
-                float* o = a.out + seq * a.o_ss + head * a.o_hs + pvd;
-                const float* z = a.gate ? a.gate + seq * a.g_ss + head * a.g_hs + pvd : nullptr;
-                float y[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    y[e] = acc[h][e] / lsum[h];
-                    if (z) y[e] = gate_mul(y[e], z[e]);
-                }
-                *reinterpret_cast<f4*>(o) = f4{y[0], y[1], y[2], y[3]};
-                *reinterpret_cast<f4*>(o + 4) = f4{y[4], y[5], y[6], y[7]};
+                float* d = pp + 8 + h * D + pvd;
+                *reinterpret_cast<f4*>(d) = f4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+                *reinterpret_cast<f4*>(d + 4) = f4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
             }
         }
-        return;
-    }
-
-    float* pp = a.part + (((int64_t)seq * a.KV + kh) * a.max_splits + s) * DEC_PART;
-    if (lane < 4) {
-        pp[lane] = ml_lds[0][lane];
-        pp[4 + lane] = ml_lds[1][lane];
-    }
-    if (lane < 32) {
+    } else {
+        // merge of the W waves in wave order: thread t handles the values v = t + 64 W k of acc[head][dim]
+        if (lane < 32) {
 #pragma unroll
-        for (int h = 0; h < 4; h++) {
-            float* d = pp + 8 + h * D + pvd;
-            *reinterpret_cast<f4*>(d) = f4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
-            *reinterpret_cast<f4*>(d + 4) = f4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+            for (int h = 0; h < 4; h++) {
+                float* d = &acc_lds[wave][h * D + pvd];
+                *reinterpret_cast<f4*>(d) = f4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+                *reinterpret_cast<f4*>(d + 4) = f4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
+            }
+        }
+        __syncthreads();
+        constexpr int VPT = 4 * D / (64 * W);  // values per thread
+        float* pp = ns == 1 ? nullptr : a.part + ((int64_t)kh * a.units + b) * DEC_PART;
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            const int v = threadIdx.x + 64 * W * k;
+            const int h = v / D, d = v % D;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < W; w++) M = fmaxf(M, ml_lds[w][0][h]);
+            float lsum = 0.0f, y = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; w++) {
+                const float mw = ml_lds[w][0][h];
+                const float wt = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+                lsum = fmaf(ml_lds[w][1][h], wt, lsum);
+                y = fmaf(acc_lds[w][v], wt, y);
+            }
+            if (ns == 1) {
+                const int head = kh * 4 + h;
+                y = y / lsum;
+                if (a.gate) y = gate_mul(y, a.gate[seq * a.g_ss + head * a.g_hs + d]);
+                a.out[seq * a.o_ss + head * a.o_hs + d] = y;
+            } else {
+                pp[8 + v] = y;
+                if (d == 0) {
+                    pp[h] = M;
+                    pp[4 + h] = lsum;
+                }
+            }
         }
     }
 }
 
 // Merge of the split partials of one (sequence, kv head): M = max m_s, L = sum l_s 2^(m_s - M),
-// out = (sum acc_s 2^(m_s - M)) / L, in split order (attn_combine.comp:10-20), then the gate.
+// out = (sum acc_s 2^(m_s - M)) / L (attn_combine.comp:10-20), then the gate. The accumulators are summed in
+// split order; the m/l terms are reduced across the wave in a fixed order, so results are reproducible.
 // Runs as its own launch after decode_split_kernel, so the partials are visible without device-wide fences.
-// Block = one wave per (head, kv head, sequence); lane: dims 4*lane .. +3.
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeArgs a) {
-    const int h = blockIdx.x, kh = blockIdx.y, seq = blockIdx.z;
-    const int lane = threadIdx.x, d0 = lane * 4;
-    const int L = min(a.kv_len ? a.kv_len[seq] : a.len0 + seq * a.len_step, a.max_len);
-    const int ns = L > 0 ? (L + a.chunk - 1) / a.chunk : 0;
+// Block = 4 waves per (sequence, kv head), wave = query head; lane: dims 4*lane .. +3, and split
+// base + lane for the m/l terms.
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+    const int seq = blockIdx.x, kh = blockIdx.y;
+    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, d0 = lane * 4;
+    const DecSplit sp = dec_find_seq(a, seq, lane);
+    const int ns = sp.n;
     if (ns <= 1) return;  // written by the split kernel
-    const float* pb = a.part + ((int64_t)seq * a.KV + kh) * a.max_splits * DEC_PART;
+    const int head = kh * 4 + h;
+    f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.gate) z = *reinterpret_cast<const f4*>(a.gate + seq * a.g_ss + head * a.g_hs + d0);
+    const float* pb = a.part + ((int64_t)kh * a.units + sp.P) * DEC_PART;
+    const float* pa = pb + 8 + h * D + d0;
+    // the first 16 splits' accumulators are requested before anything waits, together with the m terms
+    constexpr int PRE = 16;
+    f4 pre[PRE];
+#pragma unroll
+    for (int u = 0; u < PRE; u++)
+        pre[u] = u < ns ? *reinterpret_cast<const f4*>(pa + (int64_t)u * DEC_PART) : f4{0.0f, 0.0f, 0.0f, 0.0f};
     float M = -INFINITY;
-    for (int sp = lane; sp < ns; sp += 64) M = fmaxf(M, pb[(int64_t)sp * DEC_PART + h]);
+    for (int s = lane; s < ns; s += 64) M = fmaxf(M, pb[(int64_t)s * DEC_PART + h]);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
     float Ls = 0.0f;
     f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-    for (int sp = 0; sp < ns; sp++) {
-        const float* ps = pb + (int64_t)sp * DEC_PART;
-        const float w = exp2f(ps[h] - M);
-        Ls = fmaf(ps[4 + h], w, Ls);
-        const f4 v = *reinterpret_cast<const f4*>(ps + 8 + h * D + d0);
+    for (int base = 0; base < ns; base += 64) {
+        const int s = base + lane;
+        float w = 0.0f, lw = 0.0f;
+        if (s < ns) {
+            const float ms = pb[(int64_t)s * DEC_PART + h];
+            w = ms == -INFINITY ? 0.0f : exp2f(ms - M);
+            lw = pb[(int64_t)s * DEC_PART + 4 + h] * w;
+        }
 #pragma unroll
-        for (int e = 0; e < 4; e++) o[e] = fmaf(v[e], w, o[e]);
+        for (int m = 32; m >= 1; m >>= 1) lw += __shfl_xor(lw, m);
+        Ls += lw;
+        const int cnt = min(64, ns - base);
+        int j0 = 0;
+        if (base == 0) {
+#pragma unroll
+            for (int u = 0; u < PRE; u++)
+                if (u < cnt) {
+                    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o[e] = fmaf(pre[u][e], wj, o[e]);
+                }
+            j0 = PRE;
+        }
+        // eight splits' loads in flight at a time, then their products in split order
+        for (; j0 < cnt; j0 += 8) {
+            f4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (j0 + u < cnt) v[u] = *reinterpret_cast<const f4*>(pa + (int64_t)(base + j0 + u) * DEC_PART);
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (j0 + u < cnt) {
+                    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j0 + u));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) o[e] = fmaf(v[u][e], wj, o[e]);
+                }
+        }
     }
-    const int head = kh * 4 + h;
-    const float* z = a.gate ? a.gate + seq * a.g_ss + head * a.g_hs + d0 : nullptr;
     f4 y;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         y[e] = o[e] / Ls;
-        if (z) y[e] = gate_mul(y[e], z[e]);
+        if (a.gate) y[e] = gate_mul(y[e], z[e]);
     }
     *reinterpret_cast<f4*>(a.out + seq * a.o_ss + head * a.o_hs + d0) = y;
 }

@@ -163,11 +163,28 @@ def make_ragged(seed, nseq, H, KV, lo, hi):
     return lens, offs, kc, vc, q, k_new, v_new, z
 
 
-@pytest.mark.parametrize("nseq,lo,hi", [(1, 1, 1), (7, 1, 300), (32, 1024, 4096), (5, 4000, 20000)])
+@pytest.mark.parametrize("nseq,lo,hi", [(1, 1, 1), (7, 1, 300), (32, 1024, 4096), (5, 4000, 20000),
+                                        (100, 1, 400), (130, 60, 70)])
 def test_ragged_decode(gpu, nseq, lo, hi):
+    run_ragged(gpu, *make_ragged(nseq * 1000 + hi, nseq, 16, 4, lo, hi))
+
+
+def test_ragged_decode_one_long_many_short(gpu):
+    """Balanced splits on a lopsided batch: one 30000-key sequence among 70 short ones (the long one takes
+    most of the splits; more than 64 sequences take the multi-pass scan of the lengths)."""
+    nseq, H, KV = 71, 8, 2
+    lens, offs, kc, vc, q, k_new, v_new, z = make_ragged(4711, nseq, H, KV, 1, 90)
+    lens[37] = 30000
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    rows = int(lens.sum())
+    kc = oracle.f32_to_f16(oracle.rms_rows(oracle.normal(4711, 2, (rows, KV, 256))))
+    vc = oracle.f32_to_f16(oracle.normal(4711, 3, (rows, KV, 256)))
+    run_ragged(gpu, lens, offs, kc, vc, q, k_new, v_new, z)
+
+
+def run_ragged(gpu, lens, offs, kc, vc, q, k_new, v_new, z):
     torch, ctx, ws = gpu
-    H, KV = 16, 4
-    lens, offs, kc, vc, q, k_new, v_new, z = make_ragged(nseq * 1000 + hi, nseq, H, KV, lo, hi)
+    nseq, H = q.shape[0], q.shape[1]
     kc_ref, vc_ref = kc.copy(), vc.copy()
     for i in range(nseq):  # the new row of sequence i goes to its last row
         r = offs[i] + lens[i] - 1

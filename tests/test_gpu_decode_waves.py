@@ -1,0 +1,45 @@
+"""Parity of the decode split kernel built with several waves per block (merged through LDS) with the oracle.
+
+The context reads the wave count from BONSAI_ATTN_DECODE_WAVES when it is created; each fixture instance makes
+a context for one count, so every instantiation of the kernel (2, 4, 8, 16 waves) is checked on single-sequence
+decodes of several lengths (empty waves, partial last tiles, one split or many) and on ragged batches.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import workload
+from test_gpu_attn import check_case, make_ragged, run_ragged
+from glimpse_language_amd import bonsai_attn as ba
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", params=[2, 4, 8, 16])
+def wgpu(gpu, request):
+    torch, _, _ = gpu
+    old = os.environ.get("BONSAI_ATTN_DECODE_WAVES")
+    os.environ["BONSAI_ATTN_DECODE_WAVES"] = str(request.param)
+    try:
+        ctx = ba.Context(0)
+    finally:
+        if old is None:
+            del os.environ["BONSAI_ATTN_DECODE_WAVES"]
+        else:
+            os.environ["BONSAI_ATTN_DECODE_WAVES"] = old
+    ws = ba.Workspace(ctx, "cuda")
+    yield torch, ctx, ws
+    torch.cuda.synchronize()
+    ctx.close()
+
+
+@pytest.mark.parametrize("L", [1, 17, 64, 65, 1000, 4097, 20000])
+def test_decode_waves_lengths(wgpu, L):
+    inp = workload.layer(8000 + L, T=1, off=L - 1, H=8, KV=2)
+    check_case(wgpu, inp, ba.KIND_DECODE)
+
+
+@pytest.mark.parametrize("nseq,lo,hi", [(32, 1024, 4096), (100, 1, 400), (3, 5000, 9000)])
+def test_decode_waves_ragged(wgpu, nseq, lo, hi):
+    run_ragged(wgpu, *make_ragged(nseq * 1000 + hi + 7, nseq, 16, 4, lo, hi))
