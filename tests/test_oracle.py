@@ -295,3 +295,34 @@ def test_gate_rotate_is_scaled_sylvester_hadamard():
         x = attn[t].astype(np.float64) / (1.0 + np.exp(-g)) * signs
         ref = np.concatenate([Hm @ x[b:b + 512] for b in range(0, W, 512)])
         assert np.max(np.abs(xr[t] - ref)) < 2e-5
+
+
+def test_argmax_check_flags_flips_and_excuses_only_ties():
+    """The projected-argmax check of the GPU tests: a flip of a clear winner is reported, a flip between two
+    columns whose reference values tie (within 1e-4 relative) is not, identical outputs report nothing."""
+    rng = np.random.default_rng(3)
+    H, T = 4, 6
+    R = workload.projection(H)
+    ref = rng.standard_normal((T, H, 256)).astype(np.float32)
+    bad, ties = workload.argmax_mismatches(ref, ref, R)
+    assert len(bad) == 0
+    proj = ref.reshape(T, -1).astype(np.float64) @ R
+    top = np.argmax(proj, axis=1)
+    # row 0: push the runner-up far past the winner along its column direction -> a real mismatch
+    second = np.argsort(proj[0])[-2]
+    gap = proj[0, top[0]] - proj[0, second]
+    col = R[:, second] / np.dot(R[:, second], R[:, second])
+    out = ref.copy()
+    out[0] = (ref[0].reshape(-1) + (gap + 1.0) * col).reshape(H, 256)
+    bad, _ = workload.argmax_mismatches(out, ref, R)
+    assert list(bad) == [0]
+    # row 1: make the reference a tie between its two best columns, then let the output prefer the other one
+    second = np.argsort(proj[1])[-2]
+    d = R[:, top[1]] - R[:, second]
+    shift = (proj[1, top[1]] - proj[1, second]) / np.dot(d, d)
+    tie_ref = ref.copy()
+    tie_ref[1] = (ref[1].reshape(-1) - shift * d * (1 - 1e-7)).reshape(H, 256)
+    out = tie_ref.copy()
+    out[1] = (tie_ref[1].reshape(-1) - 1e-6 * d).reshape(H, 256)
+    bad, ties = workload.argmax_mismatches(out, tie_ref, R)
+    assert 1 in ties and len(bad) == 0

@@ -53,3 +53,22 @@ def projection(H):
 def projected_argmax(out, R):
     T = out.shape[0]
     return np.argmax(out.reshape(T, -1).astype(np.float64) @ R, axis=1)
+
+
+# Relative top-2 margin below which a reference row counts as a tie: fp16 keys, values and probabilities perturb an
+# output element by about 1e-5, which moves a projected value (2048 N(0,1) weights per column) by about 5e-4, i.e.
+# 5e-5 of a typical top value (about 10). A row whose two best projected values lie closer than 1e-4 of the top one
+# can swap under any fp16 implementation, so its argmax is not compared.
+TIE_REL = 1e-4
+
+
+def argmax_mismatches(out, ref, R):
+    """Rows whose projected argmax differs between `out` and `ref`, and the reference rows that are ties (top-2
+    margin below TIE_REL of the top value) and therefore not compared. Returns (mismatched rows, tie rows)."""
+    T = ref.shape[0]
+    pr = ref.reshape(T, -1).astype(np.float64) @ R
+    po = out.reshape(T, -1).astype(np.float64) @ R
+    top2 = np.sort(pr, axis=1)[:, -2:]
+    tie = (top2[:, 1] - top2[:, 0]) < TIE_REL * np.abs(top2[:, 1])
+    diff = np.argmax(po, axis=1) != np.argmax(pr, axis=1)
+    return np.nonzero(diff & ~tie)[0], np.nonzero(tie)[0]
