@@ -97,9 +97,20 @@ DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len, int64_t known_
     return p;
 }
 
-// A single-row call (T == 1): one sequence of off+1 keys.
-DecodePlan plan_one(const bn_attn_args* a, int64_t waves, int64_t target_waves) {
-    return plan_decode(1, a->KV, (int64_t)a->off + 1, (int64_t)a->off + 1, waves, target_waves);
+// T query rows of one sequence run as T single-token decodes: row t attends to off + t + 1 keys (causal among the
+// rows). The lengths are known on the host, so the split count is exact.
+DecodePlan plan_rows(const bn_attn_args* a, int64_t waves, int64_t target_waves) {
+    const int64_t T = a->T, off = a->off;
+    DecodePlan p = plan_decode(T, a->KV, off + T, T == 1 ? off + 1 : -1, waves, target_waves);
+    if (T > 1) {
+        const int64_t sum = T * (off + 1) + T * (T - 1) / 2;
+        const int64_t chunk = bn::dec_chunk(sum, (int)p.target, (int)(off + T));
+        p.units = 0;
+        for (int64_t t = 0; t < T; t++) p.units += ceil_div(off + 1 + t, chunk);
+        p.multi = p.units > T;
+        p.part_bytes = (size_t)(a->KV * p.units) * bn::DEC_PART * sizeof(float);
+    }
+    return p;
 }
 
 // T >= 2 rows: q-tiles of 32 tokens; the key range of a q-tile is split only when the q-tiles alone give
@@ -266,9 +277,16 @@ void bind_workspace(bn::DecodeArgs& d, const DecodePlan& p, void* ws) {
     d.part = p.multi ? static_cast<float*>(ws) : nullptr;
 }
 
-// One query row: the decode kernel with the append fused (the new row is the last key).
-bn_status run_decode(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
-    DecodePlan p = plan_one(a, ctx->decode_waves, ctx->decode_target_waves);
+// Query rows as single-token decodes (row t over off + t + 1 keys, the sequence's rows at stride q_ts). One row
+// fuses its append into the split kernel (the new row is its last key); several rows append first, since row t
+// reads the new rows before it from the cache.
+bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    DecodePlan p = plan_rows(a, ctx->decode_waves, ctx->decode_target_waves);
+    const bool fused = a->T == 1;
+    if (!fused && a->k_new) {
+        bn_status s = launch_append(ctx, st, a);
+        if (s) return s;
+    }
     bn::DecodeArgs d{};
     if (a->flags & BN_Q_F16)
         d.q16 = static_cast<const uint16_t*>(a->q);
@@ -276,15 +294,15 @@ bn_status run_decode(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
         d.q = static_cast<const float*>(a->q);
     d.q_ss = a->q_ts;
     d.q_hs = a->q_hs;
-    d.k_new = a->k_new;
-    d.v_new = a->v_new;
+    d.k_new = fused ? a->k_new : nullptr;
+    d.v_new = fused ? a->v_new : nullptr;
     d.kn_ss = (int64_t)a->KV * bn::D;
     d.kc = a->kc;
     d.vc = a->vc;
     d.row0 = 0;
     d.row_step = 0;
     d.len0 = (int32_t)a->off + 1;
-    d.len_step = 0;
+    d.len_step = 1;
     d.gate = a->gate;
     d.g_ss = a->g_ts;
     d.g_hs = a->g_hs;
@@ -398,8 +416,11 @@ bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     return launched(ctx, "flash_combine_kernel");
 }
 
-bn_status run(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
-    return a->T == 1 ? run_decode(ctx, st, a) : run_flash(ctx, st, a);
+// kind: 0 forward, 1 decode, 2 verify, 3 prefill. One row is always a decode; verify-sized calls (T <= 16) of the
+// forward and verify entry points run as decodes of their rows; the rest take the MFMA prefill kernels.
+bn_status run(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int kind) {
+    if (a->T == 1 || (kind != 3 && a->T <= (uint32_t)kVerifyMax)) return run_rows(ctx, st, a);
+    return run_flash(ctx, st, a);
 }
 
 }  // namespace
@@ -462,11 +483,13 @@ const char* bn_ctx_last_error(const bn_ctx* ctx) { return ctx ? ctx->err : g_che
 
 size_t bn_attn_workspace_size(const bn_attn_args* a) {
     if (!a || a->KV < 1 || a->T < 1) return 0;
-    if (a->T == 1) return plan_one(a, 1, BN_DECODE_MAX_TARGET_WAVES).total();
+    const size_t rows = a->T <= (uint32_t)kVerifyMax ? plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES).total() : 0;
+    if (a->T == 1) return rows;
     // the kernel choice for T >= 2 depends on the context, so the size covers both families
     const size_t f2 = a->T >= (uint32_t)bn::F2_BQ ? plan_flash2(a->T, a->off, a->KV).total() : 0;
     const size_t f1 = plan_flash(a->T, a->off, a->KV).total();
-    return f1 > f2 ? f1 : f2;
+    const size_t fl = f1 > f2 ? f1 : f2;
+    return fl > rows ? fl : rows;
 }
 
 size_t bn_ragged_workspace_size(const bn_ragged_args* a) {
@@ -502,28 +525,28 @@ bn_status bn_attn_decode(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_attn(a, 1, ctx->err);
     if (s) return s;
-    return run(ctx, (hipStream_t)stream, a);
+    return run(ctx, (hipStream_t)stream, a, 1);
 }
 
 bn_status bn_attn_verify(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_attn(a, 2, ctx->err);
     if (s) return s;
-    return run(ctx, (hipStream_t)stream, a);
+    return run(ctx, (hipStream_t)stream, a, 2);
 }
 
 bn_status bn_attn_prefill(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_attn(a, 3, ctx->err);
     if (s) return s;
-    return run(ctx, (hipStream_t)stream, a);
+    return run(ctx, (hipStream_t)stream, a, 3);
 }
 
 bn_status bn_attn_forward(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_attn(a, 0, ctx->err);
     if (s) return s;
-    return run(ctx, (hipStream_t)stream, a);
+    return run(ctx, (hipStream_t)stream, a, 0);
 }
 
 bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_args* a) {
