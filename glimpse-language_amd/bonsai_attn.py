@@ -24,7 +24,8 @@ EXPORTS = (
     "bn_ctx_create", "bn_ctx_destroy", "bn_status_str", "bn_ctx_last_error", "bn_abi_version",
     "bn_attn_workspace_size", "bn_ragged_workspace_size", "bn_attn_check", "bn_ragged_check",
     "bn_workspace_clear", "bn_attn_forward", "bn_attn_decode", "bn_attn_verify", "bn_attn_prefill",
-    "bn_attn_append", "bn_attn_decode_ragged",
+    "bn_attn_append", "bn_attn_decode_ragged", "bn_prep_check", "bn_rotate_check", "bn_attn_prep",
+    "bn_gate_rotate",
 )
 
 
@@ -51,6 +52,29 @@ class RaggedArgs(ctypes.Structure):
         ("gate", ctypes.c_void_p), ("g_ss", ctypes.c_int64), ("g_hs", ctypes.c_int64),
         ("out", ctypes.c_void_p), ("o_ss", ctypes.c_int64), ("o_hs", ctypes.c_int64),
         ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t),
+    ]
+
+
+class PrepArgs(ctypes.Structure):
+    _fields_ = [
+        ("T", ctypes.c_uint32), ("off", ctypes.c_uint32), ("H", ctypes.c_uint32), ("KV", ctypes.c_uint32),
+        ("cap", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("rot", ctypes.c_uint32), ("s1", ctypes.c_uint32),
+        ("s2", ctypes.c_uint32),
+        ("qp", ctypes.c_void_p), ("qp_ts", ctypes.c_int64), ("qp_hs", ctypes.c_int64),
+        ("kp", ctypes.c_void_p), ("vp", ctypes.c_void_p), ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p),
+        ("pos", ctypes.c_void_p), ("inv_freq", ctypes.c_void_p),
+        ("q", ctypes.c_void_p), ("q_ts", ctypes.c_int64), ("q_hs", ctypes.c_int64),
+        ("kc", ctypes.c_void_p), ("vc", ctypes.c_void_p),
+    ]
+
+
+class RotateArgs(ctypes.Structure):
+    _fields_ = [
+        ("T", ctypes.c_uint32), ("H", ctypes.c_uint32),
+        ("attn", ctypes.c_void_p), ("a_ts", ctypes.c_int64),
+        ("gate", ctypes.c_void_p), ("g_ts", ctypes.c_int64), ("g_hs", ctypes.c_int64),
+        ("signs", ctypes.c_void_p),
+        ("xr", ctypes.c_void_p), ("x_ts", ctypes.c_int64),
     ]
 
 
@@ -92,6 +116,14 @@ def load(path=LIB_PATH):
         f.restype = ctypes.c_int
     lib.bn_attn_decode_ragged.argtypes = [P, P, ctypes.POINTER(RaggedArgs)]
     lib.bn_attn_decode_ragged.restype = ctypes.c_int
+    lib.bn_prep_check.argtypes = [ctypes.POINTER(PrepArgs)]
+    lib.bn_prep_check.restype = ctypes.c_int
+    lib.bn_rotate_check.argtypes = [ctypes.POINTER(RotateArgs)]
+    lib.bn_rotate_check.restype = ctypes.c_int
+    lib.bn_attn_prep.argtypes = [P, P, ctypes.POINTER(PrepArgs)]
+    lib.bn_attn_prep.restype = ctypes.c_int
+    lib.bn_gate_rotate.argtypes = [P, P, ctypes.POINTER(RotateArgs)]
+    lib.bn_gate_rotate.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -202,6 +234,10 @@ def check(args, kind=KIND_FORWARD):
     lib = load()
     if isinstance(args, RaggedArgs):
         return lib.bn_ragged_check(ctypes.byref(args))
+    if isinstance(args, PrepArgs):
+        return lib.bn_prep_check(ctypes.byref(args))
+    if isinstance(args, RotateArgs):
+        return lib.bn_rotate_check(ctypes.byref(args))
     return lib.bn_attn_check(ctypes.byref(args), kind)
 
 
@@ -263,3 +299,56 @@ def decode_ragged(ctx, ws, q, kc, vc, kv_off, kv_len, max_len, out=None, k_new=N
     a.ws_bytes = 0 if buf is None else buf.numel()
     ctx.call("bn_attn_decode_ragged", a, stream)
     return out
+
+
+def prep_args(qp, kp, vp, q_norm, k_norm, pos, inv_freq, q, kc, vc, off, rot=64, s1=11, s2=11):
+    """bn_prep_args from tensors. qp: [T, H, >=256] with unit stride in the last dim (the q_proj output
+    [T, H, 512] as it is); kp/vp [T, KV, 256]; pos int32 [3, T]; q [T, H, 256] fp32 or fp16 (BN_Q_F16)."""
+    import torch
+    a = PrepArgs()
+    T, H = qp.shape[0], qp.shape[1]
+    a.T, a.off, a.H, a.KV, a.cap = T, off, H, kc.shape[1], kc.shape[0]
+    a.flags = BN_Q_F16 if q.dtype == torch.float16 else 0
+    a.rot, a.s1, a.s2 = rot, s1, s2
+    a.qp, a.qp_ts, a.qp_hs = _ptr(qp), qp.stride(0), qp.stride(1)
+    a.kp, a.vp, a.q_norm, a.k_norm = _ptr(kp), _ptr(vp), _ptr(q_norm), _ptr(k_norm)
+    a.pos, a.inv_freq = _ptr(pos), _ptr(inv_freq)
+    a.q, a.q_ts, a.q_hs = _ptr(q), q.stride(0), q.stride(1)
+    a.kc, a.vc = _ptr(kc), _ptr(vc)
+    return a
+
+
+def attn_prep(ctx, qp, kp, vp, q_norm, k_norm, pos, inv_freq, kc, vc, off, rot=64, s1=11, s2=11, q=None,
+              q_dtype=None, stream=None):
+    """attn_prep: writes normed, rotated q (returned) and the fp16 K/V cache rows [off, off + T)."""
+    import torch
+    T, H = qp.shape[0], qp.shape[1]
+    if q is None:
+        q = torch.empty((T, H, D), dtype=q_dtype or torch.float32, device=qp.device)
+    ctx.call("bn_attn_prep", prep_args(qp, kp, vp, q_norm, k_norm, pos, inv_freq, q, kc, vc, off, rot, s1, s2),
+             stream)
+    return q
+
+
+def rotate_args(attn, signs, xr, gate=None):
+    """bn_rotate_args from tensors: attn/xr [T, W] or [T, H, 256] (unit stride inside a row), gate a view
+    [T, H, 256] with unit stride in the last dim (e.g. qp[:, :, 256:]) or None."""
+    a = RotateArgs()
+    T = attn.shape[0]
+    W = signs.numel()
+    a.T, a.H = T, W // D
+    a.attn, a.a_ts = _ptr(attn), attn.stride(0)
+    a.gate = _ptr(gate)
+    a.g_ts, a.g_hs = (gate.stride(0), gate.stride(1)) if gate is not None else (0, 0)
+    a.signs = _ptr(signs)
+    a.xr, a.x_ts = _ptr(xr), xr.stride(0)
+    return a
+
+
+def gate_rotate(ctx, attn, signs, gate=None, xr=None, stream=None):
+    """gate_rotate: xr = H_512 (attn * sigmoid(gate) * signs) / sqrt(512) per 512-element block (returned)."""
+    import torch
+    if xr is None:
+        xr = torch.empty((attn.shape[0], signs.numel()), dtype=torch.float32, device=attn.device)
+    ctx.call("bn_gate_rotate", rotate_args(attn, signs, xr, gate), stream)
+    return xr

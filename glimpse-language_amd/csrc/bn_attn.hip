@@ -13,6 +13,7 @@
 #include "bn_flash.h"
 #include "bn_flash2.h"
 #include "bn_prefill.h"
+#include "bn_prep.h"
 #include "bn_util_kernels.h"
 
 struct bn_ctx {
@@ -235,6 +236,47 @@ bn_status check_ragged(const bn_ragged_args* a, char* why) {
     size_t need = bn_ragged_workspace_size(a);
     if (need && (!a->ws || a->ws_bytes < need || !aligned16(a->ws)))
         return set_err(why, BN_ENOWS, "workspace needs %zu bytes (16-byte aligned), got %zu", need, a->ws_bytes);
+    return BN_OK;
+}
+
+bn_status check_prep(const bn_prep_args* a, char* why) {
+    if (!a) return set_err(why, BN_EINVAL, "args is NULL");
+    if (a->KV < 1 || a->H != 4 * a->KV)
+        return set_err(why, BN_EINVAL, "need H == 4*KV >= 4 (H=%u KV=%u)", a->H, a->KV);
+    if (a->H + 2 * a->KV > 4u * 65535u) return set_err(why, BN_EINVAL, "too many heads (H=%u)", a->H);
+    if (a->T < 1) return set_err(why, BN_EINVAL, "T must be >= 1");
+    if ((uint64_t)a->off + a->T > a->cap)
+        return set_err(why, BN_EINVAL, "off + T = %llu exceeds cap = %u", (unsigned long long)a->off + a->T, a->cap);
+    if ((int64_t)a->off + a->T > kMaxRows) return set_err(why, BN_EINVAL, "off + T beyond %lld", (long long)kMaxRows);
+    if (a->flags & ~BN_Q_F16) return set_err(why, BN_EINVAL, "unknown flags 0x%x", a->flags);
+    if ((a->rot & 7) || a->rot > (uint32_t)bn::D)
+        return set_err(why, BN_EINVAL, "rot must be a multiple of 8 in 0..256 (rot=%u)", a->rot);
+    if (!a->qp || !a->kp || !a->vp || !a->q_norm || !a->k_norm || !a->q || !a->kc || !a->vc)
+        return set_err(why, BN_EINVAL, "qp, kp, vp, q_norm, k_norm, q, kc and vc are required");
+    if (a->rot && (!a->pos || !a->inv_freq)) return set_err(why, BN_EINVAL, "pos and inv_freq are required when rot > 0");
+    if (!aligned16(a->qp) || !aligned16(a->kp) || !aligned16(a->vp) || !aligned16(a->q_norm) ||
+        !aligned16(a->k_norm) || !aligned16(a->q) || !aligned16(a->kc) || !aligned16(a->vc))
+        return set_err(why, BN_EINVAL, "qp, kp, vp, q_norm, k_norm, q, kc and vc must be 16-byte aligned");
+    if (a->qp_ts < 0 || a->qp_hs < 0 || (a->qp_ts & 3) || (a->qp_hs & 3) || a->q_ts < 0 || a->q_hs < 0 ||
+        (a->q_ts & 3) || (a->q_hs & 3))
+        return set_err(why, BN_EINVAL, "qp and q strides must be non-negative multiples of 4 elements");
+    if ((const void*)a->qp == a->q && ((a->flags & BN_Q_F16) || a->qp_ts != a->q_ts || a->qp_hs != a->q_hs))
+        return set_err(why, BN_EINVAL, "q may be qp itself only in fp32 with the same strides");
+    return BN_OK;
+}
+
+bn_status check_rotate(const bn_rotate_args* a, char* why) {
+    if (!a) return set_err(why, BN_EINVAL, "args is NULL");
+    if (a->T < 1 || a->T > (1u << 30)) return set_err(why, BN_EINVAL, "T must be in 1..2^30");
+    if (a->H < 2 || (a->H & 1) || a->H > 2u * 65535u)
+        return set_err(why, BN_EINVAL, "H must be even, 2..131070 (H=%u)", a->H);
+    if (!a->attn || !a->signs || !a->xr) return set_err(why, BN_EINVAL, "attn, signs and xr are required");
+    if (((uintptr_t)a->attn & 3) || ((uintptr_t)a->signs & 3) || ((uintptr_t)a->xr & 3) || ((uintptr_t)a->gate & 3))
+        return set_err(why, BN_EINVAL, "attn, gate, signs and xr must be 4-byte aligned");
+    if (a->a_ts < 0 || a->x_ts < 0 || (a->gate && (a->g_ts < 0 || a->g_hs < 0)))
+        return set_err(why, BN_EINVAL, "strides must be non-negative");
+    if ((const float*)a->xr == a->attn && a->x_ts != a->a_ts)
+        return set_err(why, BN_EINVAL, "xr may be attn itself only with the same stride");
     return BN_OK;
 }
 
@@ -574,6 +616,63 @@ bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_a
     d.KV = (int)a->KV;
     bind_workspace(d, p, a->ws);
     return launch_decode(ctx, (hipStream_t)stream, d, p);
+}
+
+bn_status bn_prep_check(const bn_prep_args* a) { return check_prep(a, g_check_err); }
+
+bn_status bn_rotate_check(const bn_rotate_args* a) { return check_rotate(a, g_check_err); }
+
+bn_status bn_attn_prep(bn_ctx* ctx, bn_stream stream, const bn_prep_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_prep(a, ctx->err);
+    if (s) return s;
+    bn::PrepArgs p{};
+    p.qp = a->qp;
+    p.qp_ts = a->qp_ts;
+    p.qp_hs = a->qp_hs;
+    p.kp = a->kp;
+    p.vp = a->vp;
+    p.qn = a->q_norm;
+    p.kn = a->k_norm;
+    p.pos = a->pos;
+    p.inv_freq = a->inv_freq;
+    if (a->flags & BN_Q_F16)
+        p.q16 = static_cast<uint16_t*>(a->q);
+    else
+        p.q = static_cast<float*>(a->q);
+    p.q_ts = a->q_ts;
+    p.q_hs = a->q_hs;
+    p.kc = a->kc;
+    p.vc = a->vc;
+    p.T = (int)a->T;
+    p.off = (int)a->off;
+    p.H = (int)a->H;
+    p.KV = (int)a->KV;
+    p.rot = (int)a->rot;
+    p.s1 = (int)a->s1;
+    p.s2 = (int)a->s2;
+    const dim3 grid(a->T, (unsigned)ceil_div(a->H + 2 * a->KV, 4));
+    hipLaunchKernelGGL(bn::prep_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+    return launched(ctx, "prep_kernel");
+}
+
+bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_rotate(a, ctx->err);
+    if (s) return s;
+    bn::RotateArgs r{};
+    r.attn = a->attn;
+    r.a_ts = a->a_ts;
+    r.gate = a->gate;
+    r.g_ts = a->g_ts;
+    r.g_hs = a->g_hs;
+    r.signs = a->signs;
+    r.xr = a->xr;
+    r.x_ts = a->x_ts;
+    r.T = (int)a->T;
+    r.W = (int)a->H * bn::D;
+    hipLaunchKernelGGL(bn::rotate_kernel, dim3(a->T, a->H / 2), dim3(64), 0, (hipStream_t)stream, r);
+    return launched(ctx, "rotate_kernel");
 }
 
 }  // extern "C"

@@ -106,6 +106,52 @@ typedef struct bn_ragged_args {
     size_t ws_bytes;
 } bn_ragged_args;
 
+/* The step before attention for T rows (kernels/attn_prep.comp:29-59, dispatched at model.rs:828-851):
+ *   q = rope(rmsnorm(qp) * q_norm), k = rope(rmsnorm(kp) * k_norm), v = vp;
+ *   rmsnorm(x) = x / sqrt(mean(x^2) + 1e-6) over the 256 dims of one head (common.glsl EPS);
+ *   rope: interleaved mRoPE on dims d < rot, pairs (d, d + rot/2) with pair index i = d mod rot/2 turned by
+ *   angle pos[sel][t] * inv_freq[i], sel = 1 if i % 3 == 1 and i < 3*s1, 2 if i % 3 == 2 and i < 3*s2, else 0;
+ *   x'[d] = x[d] cos - x[d + rot/2] sin (d < rot/2), x[d] cos + x[d - rot/2] sin (rot/2 <= d < rot).
+ * k and v are rounded to fp16 (nearest even) into cache rows [off, off + T); q goes to `q` (fp32, or fp16 bits
+ * with BN_Q_F16, the form the attention call takes with the same flag). The reference keeps the cache in fp32. */
+typedef struct bn_prep_args {
+    uint32_t T, off, H, KV, cap; /* as bn_attn_args; H == 4 * KV */
+    uint32_t flags;              /* BN_Q_F16: write q as fp16 bits */
+    uint32_t rot;                /* rotary dims: a multiple of 8, at most 256 (the runtime's 64) */
+    uint32_t s1, s2;             /* mRoPE sections of the h and w position rows (the runtime's 11, 11) */
+    const float* qp;             /* query rows before the norm: element t*qp_ts + h*qp_hs + d. The runtime's q_proj
+                                    output [T][H][512] is used in place: qp_ts = 512 H, qp_hs = 512 */
+    int64_t qp_ts, qp_hs;
+    const float* kp;             /* [T][KV][256] k_proj output */
+    const float* vp;             /* [T][KV][256] v_proj output */
+    const float* q_norm;         /* [256] */
+    const float* k_norm;         /* [256] */
+    const int32_t* pos;          /* device [3][T]: the t, h and w position rows (unused when rot == 0) */
+    const float* inv_freq;       /* device [rot / 2] */
+    void* q;                     /* out: element t*q_ts + h*q_hs + d. May be qp itself with the same strides
+                                    (fp32): every row is read before it is written */
+    int64_t q_ts, q_hs;
+    uint16_t* kc;                /* [cap][KV][256] fp16 caches; rows [off, off + T) are written */
+    uint16_t* vc;
+} bn_prep_args;
+
+/* The step after attention (kernels/gate_rotate.comp:11-26, dispatched at model.rs:878-893) without its LoRA-A
+ * rows: for each row t and each block of 512 elements (two heads, e = h*256 + d),
+ *   v[e] = attn[e] * sigmoid(gate[h][d]) * signs[e],   xr = H_512 v / sqrt(512)
+ * with H_512 the Walsh-Hadamard matrix (common.glsl:55-72 fwht512). With gate == NULL attn is taken as already
+ * gated (bn_attn_forward with a gate). */
+typedef struct bn_rotate_args {
+    uint32_t T, H;               /* rows and heads; H even (W = 256 H elements per row) */
+    const float* attn;           /* element t*a_ts + e */
+    int64_t a_ts;
+    const float* gate;           /* element t*g_ts + h*g_hs + d, or NULL; the q_proj output in place:
+                                    gate = qp + 256, g_ts = 512 H, g_hs = 512 */
+    int64_t g_ts, g_hs;
+    const float* signs;          /* [W], +1 or -1 */
+    float* xr;                   /* out: element t*x_ts + e; may be attn itself with the same stride */
+    int64_t x_ts;
+} bn_rotate_args;
+
 /* ---- context ---------------------------------------------------------------------------------- */
 bn_status bn_ctx_create(int device, bn_ctx** out);
 void bn_ctx_destroy(bn_ctx* ctx);
@@ -139,6 +185,14 @@ bn_status bn_attn_append(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a);
 /* Ragged batched decode: no counterpart in the reference (one sequence per model there); each sequence
  * is the decode call above with its own cache rows. */
 bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_args* a);
+
+/* ---- either side of the attention call ------------------------------------------------------------ */
+bn_status bn_prep_check(const bn_prep_args* a);
+bn_status bn_rotate_check(const bn_rotate_args* a);
+/* attn_prep (kernels/attn_prep.comp:29-59): norms, mRoPE, fp16 K/V append. */
+bn_status bn_attn_prep(bn_ctx* ctx, bn_stream stream, const bn_prep_args* a);
+/* gate_rotate (kernels/gate_rotate.comp:11-26): gate, signs, FWHT-512, 1/sqrt(512); `xr` is o_proj's input. */
+bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a);
 
 #ifdef __cplusplus
 }

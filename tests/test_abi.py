@@ -126,3 +126,67 @@ def test_ragged_check(lib):
     assert ba.check(r) == ba.BN_OK
     r.kv_len = None
     assert ba.check(r) == ba.BN_EINVAL
+
+
+def good_prep(T=4, off=10, H=8, KV=2):
+    a = ba.PrepArgs()
+    a.T, a.off, a.H, a.KV, a.cap = T, off, H, KV, off + T
+    a.rot, a.s1, a.s2 = 64, 11, 11
+    base = 0x300000
+    a.qp, a.qp_ts, a.qp_hs = base, H * 512, 512
+    a.kp, a.vp, a.q_norm, a.k_norm = base + 0x1000, base + 0x2000, base + 0x3000, base + 0x4000
+    a.pos, a.inv_freq = base + 0x5000, base + 0x6000
+    a.q, a.q_ts, a.q_hs = base + 0x7000, H * 256, 256
+    a.kc, a.vc = base + 0x8000, base + 0x9000
+    return a
+
+
+@pytest.mark.parametrize("mutate", [
+    lambda a: setattr(a, "H", 6),                                   # not 4:1
+    lambda a: setattr(a, "T", 0),
+    lambda a: setattr(a, "cap", a.off + a.T - 1),
+    lambda a: setattr(a, "rot", 60),                                # not a multiple of 8
+    lambda a: setattr(a, "rot", 264),
+    lambda a: setattr(a, "pos", None),
+    lambda a: setattr(a, "kc", 0x308008),                           # misaligned cache
+    lambda a: setattr(a, "qp_hs", 510),
+    lambda a: setattr(a, "flags", 2),
+    lambda a: (setattr(a, "q", a.qp), setattr(a, "q_hs", 256)),     # in place with other strides
+])
+def test_prep_check(lib, mutate):
+    a = good_prep()
+    assert ba.check(a) == ba.BN_OK
+    b = good_prep()
+    b.q, b.q_ts, b.q_hs = b.qp, b.qp_ts, b.qp_hs                    # in place with the same strides is fine
+    assert ba.check(b) == ba.BN_OK
+    c = good_prep()
+    c.rot, c.pos, c.inv_freq = 0, None, None                        # no rotary dims: no positions needed
+    assert ba.check(c) == ba.BN_OK
+    mutate(a)
+    assert ba.check(a) == ba.BN_EINVAL
+    assert ba.last_check_error()
+
+
+@pytest.mark.parametrize("mutate", [
+    lambda a: setattr(a, "H", 7),                                   # blocks of 512 are two heads
+    lambda a: setattr(a, "H", 0),
+    lambda a: setattr(a, "T", 0),
+    lambda a: setattr(a, "signs", None),
+    lambda a: setattr(a, "xr", 0x400002),
+    lambda a: setattr(a, "g_hs", -1),
+    lambda a: (setattr(a, "xr", a.attn), setattr(a, "x_ts", a.a_ts + 4)),
+])
+def test_rotate_check(lib, mutate):
+    a = ba.RotateArgs()
+    a.T, a.H = 3, 16
+    base = 0x400000
+    a.attn, a.a_ts = base, 16 * 256
+    a.gate, a.g_ts, a.g_hs = base + 0x100000 + 256 * 4, 16 * 512, 512
+    a.signs = base + 0x200000
+    a.xr, a.x_ts = base + 0x300000, 16 * 256
+    assert ba.check(a) == ba.BN_OK
+    mutate(a)
+    assert ba.check(a) == ba.BN_EINVAL
+    assert ba.last_check_error()
+    assert lib.bn_rotate_check(None) == ba.BN_EINVAL
+    assert lib.bn_prep_check(None) == ba.BN_EINVAL
