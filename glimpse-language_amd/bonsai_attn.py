@@ -39,6 +39,7 @@ class AttnArgs(ctypes.Structure):
         ("gate", ctypes.c_void_p), ("g_ts", ctypes.c_int64), ("g_hs", ctypes.c_int64),
         ("out", ctypes.c_void_p), ("o_ts", ctypes.c_int64), ("o_hs", ctypes.c_int64),
         ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t),
+        ("signs", ctypes.c_void_p),
     ]
 
 
@@ -52,6 +53,7 @@ class RaggedArgs(ctypes.Structure):
         ("gate", ctypes.c_void_p), ("g_ss", ctypes.c_int64), ("g_hs", ctypes.c_int64),
         ("out", ctypes.c_void_p), ("o_ss", ctypes.c_int64), ("o_hs", ctypes.c_int64),
         ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t),
+        ("signs", ctypes.c_void_p),
     ]
 
 
@@ -190,7 +192,7 @@ def _ptr(t):
 
 
 def attn_args(T, off, H, KV, cap, q, kc, vc, out, k_new=None, v_new=None, gate=None, ws=None, flags=0,
-              q_strides=None, g_strides=None, o_strides=None):
+              q_strides=None, g_strides=None, o_strides=None, signs=None):
     """bn_attn_args from tensors. q [T][H][256] (or explicit strides), gate/out likewise; kc/vc fp16 caches
     viewed as int16/float16 tensors; ws a byte tensor or None."""
     a = AttnArgs()
@@ -205,11 +207,12 @@ def attn_args(T, off, H, KV, cap, q, kc, vc, out, k_new=None, v_new=None, gate=N
     a.o_ts, a.o_hs = o_strides if o_strides else (H * D, D)
     a.ws = _ptr(ws)
     a.ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    a.signs = _ptr(signs)
     return a
 
 
 def ragged_args(nseq, H, KV, max_len, q, kc, vc, kv_off, kv_len, out, k_new=None, v_new=None, gate=None,
-                ws=None):
+                ws=None, signs=None):
     a = RaggedArgs()
     a.nseq, a.H, a.KV, a.max_len = nseq, H, KV, max_len
     a.q, a.q_ss, a.q_hs = _ptr(q), H * D, D
@@ -220,6 +223,7 @@ def ragged_args(nseq, H, KV, max_len, q, kc, vc, kv_off, kv_len, out, k_new=None
     a.out, a.o_ss, a.o_hs = _ptr(out), H * D, D
     a.ws = _ptr(ws)
     a.ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    a.signs = _ptr(signs)
     return a
 
 
@@ -264,11 +268,12 @@ _KIND_FN = {KIND_FORWARD: "bn_attn_forward", KIND_DECODE: "bn_attn_decode", KIND
 
 
 def attention(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=None, kind=KIND_FORWARD,
-              stream=None, q_strides=None, g_strides=None):
-    """One attention-layer call: append k_new/v_new at [off, off+T), attend causally, gate.
+              stream=None, q_strides=None, g_strides=None, signs=None):
+    """One attention-layer call: append k_new/v_new at [off, off+T), attend causally, gate (and, with signs,
+    rotate: out is then o_proj's input).
 
     q: [T, H, 256] fp32, or fp16 (passed with BN_Q_F16); kc/vc: [cap, KV, 256] fp16 (torch.float16 or int16
-    view); out: [T, H, 256] fp32.
+    view); out: [T, H, 256] fp32; signs: [H * 256] fp32 +-1.
     """
     import torch
     T, H = q.shape[0], q.shape[1]
@@ -276,7 +281,8 @@ def attention(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=No
     if out is None:
         out = torch.empty((T, H, D), dtype=torch.float32, device=q.device)
     flags = BN_Q_F16 if q.dtype == torch.float16 else 0
-    a = attn_args(T, off, H, KV, cap, q, kc, vc, out, k_new, v_new, gate, None, flags, q_strides, g_strides)
+    a = attn_args(T, off, H, KV, cap, q, kc, vc, out, k_new, v_new, gate, None, flags, q_strides, g_strides,
+                  signs=signs)
     need = workspace_size(a)
     buf = ws.get(need) if ws is not None else None
     a.ws = _ptr(buf)
@@ -286,13 +292,13 @@ def attention(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=No
 
 
 def decode_ragged(ctx, ws, q, kc, vc, kv_off, kv_len, max_len, out=None, k_new=None, v_new=None, gate=None,
-                  stream=None):
+                  stream=None, signs=None):
     import torch
     nseq, H = q.shape[0], q.shape[1]
     KV = kc.shape[1]
     if out is None:
         out = torch.empty((nseq, H, D), dtype=torch.float32, device=q.device)
-    a = ragged_args(nseq, H, KV, max_len, q, kc, vc, kv_off, kv_len, out, k_new, v_new, gate)
+    a = ragged_args(nseq, H, KV, max_len, q, kc, vc, kv_off, kv_len, out, k_new, v_new, gate, signs=signs)
     need = workspace_size(a)
     buf = ws.get(need) if ws is not None else None
     a.ws = _ptr(buf)

@@ -209,6 +209,7 @@ bn_status check_attn(const bn_attn_args* a, int kind, char* why) {
         return set_err(why, BN_EINVAL, "q must be 16-byte aligned with strides that are whole 16-byte groups");
     if (a->gate && (a->g_ts < 0 || a->g_hs < 0 || ((uintptr_t)a->gate & 3)))
         return set_err(why, BN_EINVAL, "bad gate pointer or strides");
+    if (a->signs && !aligned16(a->signs)) return set_err(why, BN_EINVAL, "signs must be 16-byte aligned");
     size_t need = bn_attn_workspace_size(a);
     if (need && (!a->ws || a->ws_bytes < need || !aligned16(a->ws)))
         return set_err(why, BN_ENOWS, "workspace needs %zu bytes (16-byte aligned), got %zu", need, a->ws_bytes);
@@ -233,6 +234,7 @@ bn_status check_ragged(const bn_ragged_args* a, char* why) {
     if (a->q_ss < 0 || a->q_hs < 0 || ((uintptr_t)a->q & 3)) return set_err(why, BN_EINVAL, "bad q pointer or strides");
     if (a->gate && (a->g_ss < 0 || a->g_hs < 0 || ((uintptr_t)a->gate & 3)))
         return set_err(why, BN_EINVAL, "bad gate pointer or strides");
+    if (a->signs && !aligned16(a->signs)) return set_err(why, BN_EINVAL, "signs must be 16-byte aligned");
     size_t need = bn_ragged_workspace_size(a);
     if (need && (!a->ws || a->ws_bytes < need || !aligned16(a->ws)))
         return set_err(why, BN_ENOWS, "workspace needs %zu bytes (16-byte aligned), got %zu", need, a->ws_bytes);
@@ -351,6 +353,7 @@ bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     d.out = a->out;
     d.o_ss = a->o_ts;
     d.o_hs = a->o_hs;
+    d.signs = a->signs;
     d.KV = (int)a->KV;
     bind_workspace(d, p, a->ws);
     return launch_decode(ctx, st, d, p);
@@ -417,7 +420,7 @@ bn_status run_prefill(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
 }
 
 // T >= 2 rows: append, then the MFMA kernel (and the split merge when the key range is split).
-bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+bn_status attend_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     if (a->k_new) {
         bn_status s = launch_append(ctx, st, a);
         if (s) return s;
@@ -456,6 +459,29 @@ bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     if (s || p.max_splits == 1) return s;
     hipLaunchKernelGGL(bn::flash_combine_kernel, dim3(a->T, a->H), dim3(64), 0, st, f);
     return launched(ctx, "flash_combine_kernel");
+}
+
+// The rotation of the gated output in place (the prefill kernels write gated rows; the decode kernels rotate in
+// their own epilogue).
+bn_status rotate_in_place(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    bn::RotateArgs r{};
+    r.attn = a->out;
+    r.a_ts = a->o_ts;
+    r.a_hs = a->o_hs;
+    r.signs = a->signs;
+    r.xr = a->out;
+    r.x_ts = a->o_ts;
+    r.x_hs = a->o_hs;
+    r.T = (int)a->T;
+    r.W = (int)a->H * bn::D;
+    hipLaunchKernelGGL(bn::rotate_kernel, dim3(a->T, a->H / 2), dim3(64), 0, st, r);
+    return launched(ctx, "rotate_kernel");
+}
+
+bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    bn_status s = attend_flash(ctx, st, a);
+    if (s || !a->signs) return s;
+    return rotate_in_place(ctx, st, a);
 }
 
 // kind: 0 forward, 1 decode, 2 verify, 3 prefill. One row is always a decode; verify-sized calls (T <= 16) of the
@@ -613,6 +639,7 @@ bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_a
     d.out = a->out;
     d.o_ss = a->o_ss;
     d.o_hs = a->o_hs;
+    d.signs = a->signs;
     d.KV = (int)a->KV;
     bind_workspace(d, p, a->ws);
     return launch_decode(ctx, (hipStream_t)stream, d, p);
@@ -663,12 +690,14 @@ bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a)
     bn::RotateArgs r{};
     r.attn = a->attn;
     r.a_ts = a->a_ts;
+    r.a_hs = bn::D;
     r.gate = a->gate;
     r.g_ts = a->g_ts;
     r.g_hs = a->g_hs;
     r.signs = a->signs;
     r.xr = a->xr;
     r.x_ts = a->x_ts;
+    r.x_hs = bn::D;
     r.T = (int)a->T;
     r.W = (int)a->H * bn::D;
     hipLaunchKernelGGL(bn::rotate_kernel, dim3(a->T, a->H / 2), dim3(64), 0, (hipStream_t)stream, r);

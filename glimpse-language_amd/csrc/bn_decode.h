@@ -50,6 +50,8 @@ struct DecodeArgs {
     int64_t g_ss, g_hs;
     float* out;          // element seq*o_ss + head*o_hs + d
     int64_t o_ss, o_hs;
+    const float* signs;  // [heads*256] +-1, or null; when set, out receives each row rotated: blocks of 512
+                         // (heads 2j, 2j+1) times the signs, Walsh-Hadamard transformed, / sqrt(512)
     float* part;         // [KV][units][DEC_PART]
     int KV, nseq, max_len;
     int target;          // splits aimed at per kv head
@@ -350,15 +352,28 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
                     const int head = kh * 4 + h;
                     float* o = a.out + seq * a.o_ss + head * a.o_hs + pvd;
                     const float* z = a.gate ? a.gate + seq * a.g_ss + head * a.g_hs + pvd : nullptr;
-                    float y[8];
+                    f4 y0, y1;
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
-                        y[e] = acc[h][e] / lsum[h];
-                        if (z) y[e] = gate_mul(y[e], z[e]);
+                        float y = acc[h][e] / lsum[h];
+                        if (z) y = gate_mul(y, z[e]);
+                        if (e < 4) y0[e] = y; else y1[e - 4] = y;
                     }
-                    *reinterpret_cast<f4*>(o) = f4{y[0], y[1], y[2], y[3]};
-                    *reinterpret_cast<f4*>(o + 4) = f4{y[4], y[5], y[6], y[7]};
+                    if (a.signs) {  // staged for the rotation below
+                        const float* sg = a.signs + head * D + pvd;
+                        *reinterpret_cast<f4*>(&acc_lds[0][h * D + pvd]) = y0 * *reinterpret_cast<const f4*>(sg);
+                        *reinterpret_cast<f4*>(&acc_lds[0][h * D + pvd + 4]) = y1 * *reinterpret_cast<const f4*>(sg + 4);
+                    } else {
+                        *reinterpret_cast<f4*>(o) = y0;
+                        *reinterpret_cast<f4*>(o + 4) = y1;
+                    }
                 }
+            }
+            if (a.signs) {
+                wave_lds_sync();
+                float* o = a.out + seq * a.o_ss + (int64_t)kh * 4 * a.o_hs;
+                rotate_group_store(acc_lds[0], o, a.o_hs, 0, lane);
+                rotate_group_store(acc_lds[0], o, a.o_hs, 1, lane);
             }
             return;
         }
@@ -407,7 +422,11 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
                 const int head = kh * 4 + h;
                 y = y / lsum;
                 if (a.gate) y = gate_mul(y, a.gate[seq * a.g_ss + head * a.g_hs + d]);
-                a.out[seq * a.o_ss + head * a.o_hs + d] = y;
+                // value v is read and staged by this thread only, so the slot in acc_lds[0] is free to reuse
+                if (a.signs)
+                    acc_lds[0][v] = y * a.signs[head * D + d];
+                else
+                    a.out[seq * a.o_ss + head * a.o_hs + d] = y;
             } else {
                 pp[8 + v] = y;
                 if (d == 0) {
@@ -416,16 +435,22 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
                 }
             }
         }
+        if (ns == 1 && a.signs) {
+            __syncthreads();
+            if (wave < 2) rotate_group_store(acc_lds[0], a.out + seq * a.o_ss + (int64_t)kh * 4 * a.o_hs, a.o_hs, wave, lane);
+        }
     }
 }
 
 // Merge of the split partials of one (sequence, kv head): M = max m_s, L = sum l_s 2^(m_s - M),
-// out = (sum acc_s 2^(m_s - M)) / L (attn_combine.comp:10-20), then the gate. The accumulators are summed in
+// out = (sum acc_s 2^(m_s - M)) / L (attn_combine.comp:10-20), then the gate and, with signs, the rotation
+// (gate_rotate.comp:18-25: waves 0 and 1 each transform one 512-element block of the group). The accumulators are summed in
 // split order; the m/l terms are reduced across the wave in a fixed order, so results are reproducible.
 // Runs as its own launch after decode_split_kernel, so the partials are visible without device-wide fences.
 // Block = 4 waves per (sequence, kv head), wave = query head; lane: dims 4*lane .. +3, and split
 // base + lane for the m/l terms.
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+    __shared__ float rot_lds[4 * D];  // the group's gated rows times the signs, when the output is rotated
     const int seq = blockIdx.x, kh = blockIdx.y;
     const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, d0 = lane * 4;
     const DecSplit sp = dec_find_seq(a, seq, lane);
@@ -491,6 +516,12 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
     for (int e = 0; e < 4; e++) {
         y[e] = o[e] / Ls;
         if (a.gate) y[e] = gate_mul(y[e], z[e]);
+    }
+    if (a.signs) {
+        *reinterpret_cast<f4*>(&rot_lds[h * D + d0]) = y * *reinterpret_cast<const f4*>(a.signs + head * D + d0);
+        __syncthreads();
+        if (h < 2) rotate_group_store(rot_lds, a.out + seq * a.o_ss + (int64_t)kh * 4 * a.o_hs, a.o_hs, h, lane);
+        return;
     }
     *reinterpret_cast<f4*>(a.out + seq * a.o_ss + head * a.o_hs + d0) = y;
 }

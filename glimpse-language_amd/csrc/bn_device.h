@@ -62,4 +62,43 @@ __device__ __forceinline__ float gate_mul_fast(float a, float z) {
     return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * LOG2E));
 }
 
+// Unnormalised 512-point Walsh-Hadamard transform of v held by one wave: lane l holds elements l + 64 e
+// (e = 0..7). Index bits 0-5 are butterflies across lanes (xor shuffles), bits 6-8 inside the lane; the stages
+// commute, so the result is H_512 v in any stage order (common.glsl:55-72 fwht512 computes the same transform
+// with 32-lane subgroups and 16 elements per lane).
+__device__ __forceinline__ void fwht512_wave(float (&v)[8], int lane) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const bool up = (lane & m) != 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float o = __shfl_xor(v[e], m);
+            v[e] = up ? o - v[e] : v[e] + o;
+        }
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            if ((e & h) == 0) {
+                const float p = v[e], q = v[e + h];
+                v[e] = p + q;
+                v[e + h] = p - q;
+            }
+}
+
+constexpr float INV_SQRT512 = 0.044194173824159216f;
+
+// The rotated output of one (row, kv head) group: `lds` holds y[h*256 + d] * sign for the group's 4 heads; the
+// calling wave transforms 512-element block j (heads 2j, 2j+1) and stores it at o (the group's head 0) with head
+// stride o_hs. All 64 lanes take part.
+__device__ __forceinline__ void rotate_group_store(const float* lds, float* o, int64_t o_hs, int j, int lane) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = lds[j * 512 + lane + 64 * e];
+    fwht512_wave(v, lane);
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[(2 * j + (e >> 2)) * o_hs + lane + 64 * (e & 3)] = v[e] * INV_SQRT512;
+}
+
 }  // namespace bn

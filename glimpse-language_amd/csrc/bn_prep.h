@@ -88,50 +88,34 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
 }
 
 struct RotateArgs {
-    const float* attn;       // ungated attention output: element t*a_ts + e (e = h*256 + d)
-    int64_t a_ts;
+    const float* attn;       // attention output: element t*a_ts + h*a_hs + d
+    int64_t a_ts, a_hs;
     const float* gate;       // gate logits: element t*g_ts + h*g_hs + d, or null (attn is already gated)
     int64_t g_ts, g_hs;
-    const float* signs;      // [H*256], +-1
-    float* xr;               // element t*x_ts + e
-    int64_t x_ts;
+    const float* signs;      // [H*256], +-1, indexed by e = h*256 + d
+    float* xr;               // element t*x_ts + h*x_hs + d
+    int64_t x_ts, x_hs;
     int T, W;                // W = H * 256, a multiple of 512
 };
 
 // Grid (T, W / 512) x one wave: block b of token t is elements 512b .. 512b+511 (two heads). Lane l holds elements
-// l + 64e (e = 0..7): v = attn * sigmoid(gate) * sign, then the unnormalised Walsh-Hadamard transform over the
-// 9 index bits (bits 0-5 across lanes with xor shuffles, bits 6-8 inside the lane; the stages commute, so the
-// result is H_512 v in any stage order), then x 1/sqrt(512).
+// l + 64e (e = 0..7): v = attn * sigmoid(gate) * sign, then the unnormalised Walsh-Hadamard transform
+// (fwht512_wave), then x 1/sqrt(512).
 __global__ __launch_bounds__(64) void rotate_kernel(RotateArgs a) {
     const int t = blockIdx.x, b0 = blockIdx.y * 512, lane = threadIdx.x;
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         const int i = b0 + lane + 64 * e, hd = i >> 8, d = i & 255;
-        const float at = a.attn[t * a.a_ts + i];
+        const float at = a.attn[t * a.a_ts + hd * a.a_hs + d];
         v[e] = (a.gate ? gate_mul(at, a.gate[t * a.g_ts + hd * a.g_hs + d]) : at) * a.signs[i];
     }
+    fwht512_wave(v, lane);
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const bool up = (lane & m) != 0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float o = __shfl_xor(v[e], m);
-            v[e] = up ? o - v[e] : v[e] + o;
-        }
+    for (int e = 0; e < 8; e++) {
+        const int i = b0 + lane + 64 * e;
+        a.xr[t * a.x_ts + (i >> 8) * a.x_hs + (i & 255)] = v[e] * INV_SQRT512;
     }
-#pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            if ((e & h) == 0) {
-                const float p = v[e], q = v[e + h];
-                v[e] = p + q;
-                v[e + h] = p - q;
-            }
-    constexpr float kInvSqrt512 = 0.044194173824159216f;
-#pragma unroll
-    for (int e = 0; e < 8; e++) a.xr[t * a.x_ts + b0 + lane + 64 * e] = v[e] * kInvSqrt512;
 }
 
 }  // namespace bn

@@ -6,7 +6,8 @@
  *     attn_prep     -> K/V rows appended to the cache at [off, off + T)   (kernels/attn_prep.comp:36-39,58)
  *     attn_split    -> split-K causal GQA partials                          (kernels/attn_split.comp:9-58)
  *     attn_combine  -> log-sum-exp merge of the splits                      (kernels/attn_combine.comp:6-21)
- *     gate_rotate   -> a * sigmoid(gate)  (first half of the kernel)        (kernels/gate_rotate.comp:19-22)
+ *     gate_rotate   -> a * sigmoid(gate), and with `signs` the Hadamard     (kernels/gate_rotate.comp:19-25)
+ *                      rotation that makes o_proj's input
  * through Cmd::run (src/bonsai/runtime/gpu_vk.rs:843-882, gpu.rs:169-255). Query/key normalisation and
  * rotary embedding (the rest of attn_prep) happen before the call: q and k_new arrive post-norm, post-RoPE,
  * or go through bn_attn_prep first.
@@ -40,7 +41,7 @@ extern "C" {
 #endif
 
 #define BN_HEAD_DIM 256
-#define BN_ABI_VERSION 1
+#define BN_ABI_VERSION 2
 
 typedef enum bn_status {
     BN_OK = 0,
@@ -74,13 +75,19 @@ typedef struct bn_attn_args {
     int64_t g_ts, g_hs; /* the runtime's q_proj output [T][H][512] is used in place: gate = qp + 256,
                            g_ts = 512 * H, g_hs = 512 (gate_rotate.comp:19-20) */
 
-    float* out;         /* [T][H][256] fp32 gated attention output */
+    float* out;         /* [T][H][256] fp32 gated attention output (rotated when `signs` is set) */
     int64_t o_ts, o_hs;
 
     void* ws;        /* device workspace (split partials), >= bn_attn_workspace_size(args) bytes, 16-byte
                         aligned; NULL when the size is 0. No initialisation is needed and nothing in it
                         outlives the call. Calls that overlap in time on one workspace race. */
     size_t ws_bytes;
+
+    const float* signs; /* [H * 256] +1/-1 (16-byte aligned), or NULL. When set, `out` receives o_proj's input
+                           instead of the gated output: the rest of gate_rotate (gate_rotate.comp:22-25), i.e.
+                           per row and block of 512 elements (heads 2j, 2j+1), H_512 (gated * signs) / sqrt(512).
+                           Decode and verify calls rotate in their epilogue; prefill calls rotate in place after
+                           the attention kernel. */
 } bn_attn_args;
 
 #define BN_Q_F16 1u
@@ -104,6 +111,7 @@ typedef struct bn_ragged_args {
     int64_t o_ss, o_hs;
     void* ws;
     size_t ws_bytes;
+    const float* signs;  /* as bn_attn_args.signs */
 } bn_ragged_args;
 
 /* The step before attention for T rows (kernels/attn_prep.comp:29-59, dispatched at model.rs:828-851):

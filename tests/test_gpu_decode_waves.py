@@ -1,8 +1,9 @@
 """Parity of the decode split kernel built with several waves per block (merged through LDS) with the oracle.
 
 The context reads the wave count from BONSAI_ATTN_DECODE_WAVES when it is created; each fixture instance makes
-a context for one count, so every instantiation of the kernel (2, 4, 8, 16 waves) is checked on single-sequence
-decodes of several lengths (empty waves, partial last tiles, one split or many) and on ragged batches.
+a context for one count, so every instantiation of the kernel (1, 2, 4, 8, 16 waves) is checked on single-sequence
+decodes of several lengths (empty waves, partial last tiles, one split or many), on ragged batches and with the
+output rotated in the epilogue.
 """
 import os
 
@@ -11,12 +12,13 @@ import pytest
 
 import workload
 from test_gpu_attn import check_case, make_ragged, run_ragged
+from test_gpu_rotate_fused import check_rotated
 from glimpse_language_amd import bonsai_attn as ba
 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module", params=[2, 4, 8, 16])
+@pytest.fixture(scope="module", params=[1, 2, 4, 8, 16])
 def wgpu(gpu, request):
     torch, _, _ = gpu
     old = os.environ.get("BONSAI_ATTN_DECODE_WAVES")
@@ -43,3 +45,8 @@ def test_decode_waves_lengths(wgpu, L):
 @pytest.mark.parametrize("nseq,lo,hi", [(32, 1024, 4096), (100, 1, 400), (3, 5000, 9000)])
 def test_decode_waves_ragged(wgpu, nseq, lo, hi):
     run_ragged(wgpu, *make_ragged(nseq * 1000 + hi + 7, nseq, 16, 4, lo, hi))
+
+
+@pytest.mark.parametrize("L", [17, 1000, 20000])
+def test_decode_waves_rotated(wgpu, L):
+    check_rotated(wgpu, workload.layer(9000 + L, T=1, off=L - 1, H=8, KV=2), ba.KIND_DECODE)
