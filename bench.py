@@ -90,7 +90,11 @@ class Workloads:
         g.manual_seed(seed)
         return g
 
-    def decode_batch(self, steps, warmup, nseq=32, H=16, KV=4, lens=None, seed=0xB0A5A104):
+    def signs(self, H, seed=0xB0A5A1FF):
+        g = self._gen(seed)
+        return self.torch.randint(0, 2, (H * D,), device="cuda", generator=g).float() * 2 - 1
+
+    def decode_batch(self, steps, warmup, nseq=32, H=16, KV=4, lens=None, seed=0xB0A5A104, rotate=False):
         torch, ba, ctx = self.torch, self.ba, self.ctx
         g = self._gen(seed)
         if lens is None:
@@ -109,17 +113,18 @@ class Workloads:
         kv_len = torch.tensor(lens, device="cuda", dtype=torch.int32)
         out = torch.empty(nseq, H, D, device="cuda")
         max_len = max(lens)
+        signs = self.signs(H) if rotate else None
 
         def step():
             ba.decode_ragged(ctx, self.ws, q, kc, vc, kv_off, kv_len, max_len, out=out, k_new=k_new, v_new=v_new,
-                             gate=gate)
+                             gate=gate, signs=signs)
 
         ms, wall = time_steps(torch, step, steps, warmup)
         nbytes = decode_bytes(H, KV, lens)
         del kc, vc
         return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
-    def attn(self, steps, warmup, H, KV, T, off, kind, seed, q_f16=False):
+    def attn(self, steps, warmup, H, KV, T, off, kind, seed, q_f16=False, rotate=False):
         torch, ba, ctx = self.torch, self.ba, self.ctx
         g = self._gen(seed)
         cap = off + T
@@ -132,15 +137,58 @@ class Workloads:
         v_new = torch.randn(T, KV, D, device="cuda", generator=g)
         gate = torch.randn(T, H, D, device="cuda", generator=g)
         out = torch.empty(T, H, D, device="cuda")
+        signs = self.signs(H) if rotate else None
 
         def step():
-            ba.attention(ctx, self.ws, q, kc, vc, off, out=out, k_new=k_new, v_new=v_new, gate=gate, kind=kind)
+            ba.attention(ctx, self.ws, q, kc, vc, off, out=out, k_new=k_new, v_new=v_new, gate=gate, kind=kind,
+                         signs=signs)
 
         ms, wall = time_steps(torch, step, steps, warmup)
         flops = attn_flops(H, T, off)
         nbytes = attn_bytes(H, KV, T, off, q_bytes=2 if q_f16 else 4)
         return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12, bytes=nbytes,
                     gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
+
+
+    def prep(self, steps, warmup, H, KV, T, off, seed=0xB0A5A106):
+        """bn_attn_prep over T rows: q_proj output [T][H][512] (q half read), k/v_proj rows, norm weights,
+        positions; q out fp32, fp16 K/V rows written at [off, off + T)."""
+        torch, ba, ctx = self.torch, self.ba, self.ctx
+        g = self._gen(seed)
+        qp = torch.randn(T, H, 512, device="cuda", generator=g)
+        kp = torch.randn(T, KV, D, device="cuda", generator=g)
+        vp = torch.randn(T, KV, D, device="cuda", generator=g)
+        qn = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+        kn = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+        p = torch.arange(off, off + T, device="cuda", dtype=torch.int32)
+        pos = torch.stack([p, p, p]).contiguous()
+        inv = 1.0 / (1e7 ** (torch.arange(32, device="cuda", dtype=torch.float32) * 2 / 64))
+        kc = torch.empty(off + T, KV, D, device="cuda", dtype=torch.int16)
+        vc = torch.empty_like(kc)
+        q = torch.empty(T, H, D, device="cuda")
+
+        def step():
+            ba.attn_prep(ctx, qp, kp, vp, qn, kn, pos, inv, kc, vc, off, q=q)
+
+        ms, wall = time_steps(torch, step, steps, warmup)
+        nbytes = T * H * D * 4 * 2 + T * KV * D * 4 * 2 + T * KV * D * 2 * 2 + 3 * T * 4
+        return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
+
+    def rotate(self, steps, warmup, H, T, seed=0xB0A5A107):
+        """bn_gate_rotate over T rows: attn [T][H*256] and the gate half of the q_proj output read, xr written."""
+        torch, ba, ctx = self.torch, self.ba, self.ctx
+        g = self._gen(seed)
+        attn = torch.randn(T, H * D, device="cuda", generator=g)
+        qp = torch.randn(T, H, 512, device="cuda", generator=g)
+        signs = self.signs(H)
+        xr = torch.empty(T, H * D, device="cuda")
+
+        def step():
+            ba.gate_rotate(ctx, attn, signs, gate=qp[:, :, D:], xr=xr)
+
+        ms, wall = time_steps(torch, step, steps, warmup)
+        nbytes = 3 * T * H * D * 4 + H * D * 4
+        return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
 
 def measured_traffic(name):
@@ -193,7 +241,9 @@ def cpu_baseline(budget_s=10.0, H=16, KV=4, L=8192, nseq=2):
                       f"(oracle/bn_oracle.c, -O2, no fast-math), OpenMP {threads} threads"}
 
 
-ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix")
+ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix",
+       "decode_8k_batch32_rotated", "prefill_4k_rotated", "verify_8_rotated", "prep_4k", "prep_decode",
+       "gate_rotate_4k")
 
 
 def main():
@@ -249,6 +299,31 @@ def main():
         log("prefill_prefix")
         res["prefill_prefix"] = r = W.attn(K, Wm, 8, 2, 256, 512, ba.KIND_PREFILL, 0xB0A5A101)
         log(f"  {r['ms'] * 1e3:.1f} us/step, {r['tflops']:.2f} TFLOP/s")
+    if "decode_8k_batch32_rotated" in only:
+        log("decode_8k_batch32_rotated")
+        res["decode_8k_batch32_rotated"] = r = W.decode_batch(K, Wm, rotate=True)
+        log(f"  {r['gbs']:.1f} GB/s ({r['ms'] * 1e3:.1f} us/step)")
+    if "prefill_4k_rotated" in only:
+        log("prefill_4k_rotated")
+        res["prefill_4k_rotated"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
+                                               0xB0A5A103, q_f16=True, rotate=True)
+        log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
+    if "verify_8_rotated" in only:
+        log("verify_8_rotated")
+        res["verify_8_rotated"] = r = W.attn(K, Wm, 8, 2, 8, 2048, ba.KIND_VERIFY, 0xB0A5A102, rotate=True)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "prep_4k" in only:
+        log("prep_4k")
+        res["prep_4k"] = r = W.prep(K, Wm, 16, 4, 4096, 0)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "prep_decode" in only:
+        log("prep_decode")
+        res["prep_decode"] = r = W.prep(K, Wm, 16, 4, 1, 8191)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "gate_rotate_4k" in only:
+        log("gate_rotate_4k")
+        res["gate_rotate_4k"] = r = W.rotate(K, Wm, 16, 4096)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -287,7 +362,7 @@ def main():
                            "ms_per_step": round(pre["ms"], 5), "flops": pre["flops"], "peak": MFMA_F16_PEAK_TFLOPS,
                            "frac": round(pre["tflops"] / MFMA_F16_PEAK_TFLOPS, 5)}
     others = {}
-    for name in ("ragged_32", "verify_8", "decode_1k", "prefill_prefix"):
+    for name in ALL[2:]:
         r = res.get(name)
         if r:
             o = {"us_per_step": round(r["ms"] * 1e3, 3), "GB/s": round(r["gbs"], 2),

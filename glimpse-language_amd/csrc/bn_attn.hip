@@ -410,6 +410,7 @@ bn_status run_prefill(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     f.out = a->out;
     f.o_ts = a->o_ts;
     f.o_hs = a->o_hs;
+    f.signs = a->signs;
     f.T = (int)a->T;
     f.off = (int)a->off;
     f.KV = (int)a->KV;
@@ -461,8 +462,8 @@ bn_status attend_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     return launched(ctx, "flash_combine_kernel");
 }
 
-// The rotation of the gated output in place (the prefill kernels write gated rows; the decode kernels rotate in
-// their own epilogue).
+// The rotation of the gated output in place, after flash_kernel / flash2_kernel (the decode kernels and
+// prefill_kernel rotate in their own epilogue).
 bn_status rotate_in_place(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     bn::RotateArgs r{};
     r.attn = a->out;
@@ -479,8 +480,9 @@ bn_status rotate_in_place(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
 }
 
 bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    const bool fused = use_prefill(a, ctx->prefill_min_blocks);  // prefill_kernel rotates in its epilogue
     bn_status s = attend_flash(ctx, st, a);
-    if (s || !a->signs) return s;
+    if (s || !a->signs || fused) return s;
     return rotate_in_place(ctx, st, a);
 }
 

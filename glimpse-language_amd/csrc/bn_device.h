@@ -62,19 +62,45 @@ __device__ __forceinline__ float gate_mul_fast(float a, float z) {
     return a * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * LOG2E));
 }
 
+// x from lane (lane ^ m) for the DPP controls used below: 0xB1 quad_perm [1,0,3,2] (m = 1), 0x4E quad_perm
+// [2,3,0,1] (m = 2), 0x1B quad_perm [3,2,1,0] (m = 3), 0x141 row_half_mirror (m = 7 inside each 8 lanes), 0x128
+// row_ror:8 (m = 8 inside each row of 16)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
 // Unnormalised 512-point Walsh-Hadamard transform of v held by one wave: lane l holds elements l + 64 e
-// (e = 0..7). Index bits 0-5 are butterflies across lanes (xor shuffles), bits 6-8 inside the lane; the stages
-// commute, so the result is H_512 v in any stage order (common.glsl:55-72 fwht512 computes the same transform
-// with 32-lane subgroups and 16 elements per lane).
+// (e = 0..7). Index bits 0-5 are butterflies across lanes, bits 6-8 inside the lane; the stages commute, so the
+// result is H_512 v (common.glsl:55-72 fwht512 computes the same transform with 32-lane subgroups and 16 elements
+// per lane). A cross-lane butterfly pairs lane l with l ^ m: the lower lane needs own + partner, the upper one
+// partner - own. Every lane computes own + s partner instead (s = -1 on the upper lane), which leaves the upper
+// lane's result negated; the two lanes of a later stage have taken the same sides so far, so they carry the same
+// sign, and the signs are settled once at the end: (-1)^popcount(l). The partners come from DPP moves (m = 1, 2,
+// 4 = 7 then 3, 8) and v_permlane16/32_swap (m = 16, 32), with no LDS traffic.
 __device__ __forceinline__ void fwht512_wave(float (&v)[8], int lane) {
+    const float s1 = (lane & 1) ? -1.0f : 1.0f, s2 = (lane & 2) ? -1.0f : 1.0f, s4 = (lane & 4) ? -1.0f : 1.0f;
+    const float s8 = (lane & 8) ? -1.0f : 1.0f, s16 = (lane & 16) ? -1.0f : 1.0f, s32 = (lane & 32) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const bool up = (lane & m) != 0;
+    for (int e = 0; e < 8; e++) v[e] = fmaf(dpp_f32<0xB1>(v[e]), s1, v[e]);
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float o = __shfl_xor(v[e], m);
-            v[e] = up ? o - v[e] : v[e] + o;
-        }
+    for (int e = 0; e < 8; e++) v[e] = fmaf(dpp_f32<0x4E>(v[e]), s2, v[e]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = fmaf(dpp_f32<0x1B>(dpp_f32<0x141>(v[e])), s4, v[e]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = fmaf(dpp_f32<0x128>(v[e]), s8, v[e]);
+    // permlane16_swap(x, x): first result = rows (0, 0, 2, 2) of x, second = rows (1, 1, 3, 3); own + s partner
+    // is then first * s + second on either side
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[e]), __float_as_uint(v[e]), false, false);
+        v[e] = fmaf(__uint_as_float(r[0]), s16, __uint_as_float(r[1]));
+    }
+    // permlane32_swap(x, x): first = lanes 0-31 of x in both halves, second = lanes 32-63
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[e]), __float_as_uint(v[e]), false, false);
+        v[e] = fmaf(__uint_as_float(r[0]), s32, __uint_as_float(r[1]));
     }
 #pragma unroll
     for (int h = 1; h < 8; h <<= 1)
@@ -85,6 +111,9 @@ __device__ __forceinline__ void fwht512_wave(float (&v)[8], int lane) {
                 v[e] = p + q;
                 v[e + h] = p - q;
             }
+    const float sg = (__builtin_popcount(lane & 63) & 1) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] *= sg;
 }
 
 constexpr float INV_SQRT512 = 0.044194173824159216f;

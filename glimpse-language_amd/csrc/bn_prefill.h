@@ -1,7 +1,7 @@
 // Causal GQA prefill for long prompts on fp16 MFMA: 8 waves per block, the key range of every q-tile split
 // between two wave groups that merge through LDS.
 //
-// Semantics follow attn_split.comp:9-58 + attn_combine.comp:6-21 + gate_rotate.comp:19-22 of the reference:
+// Semantics follow attn_split.comp:9-58 + attn_combine.comp:6-21 + gate_rotate.comp:19-25 of the reference:
 // row t (position off+t) of head h attends to cache rows [0, off+t+1) of kv head h/4; softmax(q.k/16) v,
 // then a * sigmoid(gate). The K/V rows of the call are appended to the cache before this kernel runs.
 //
@@ -53,6 +53,8 @@ struct PrefillArgs {
     int64_t g_ts, g_hs;
     float* out;              // element t*o_ts + h*o_hs + d
     int64_t o_ts, o_hs;
+    const float* signs;      // [heads*256] +-1, or null: out receives each row rotated (blocks of 512 = heads
+                             // 2j, 2j+1, times the signs, Walsh-Hadamard transformed, / sqrt(512))
     int T, off, KV, ntq;
 };
 
@@ -364,6 +366,22 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                 yr[d * 1024 + (8 * (r >> 2) + 4 * h + (r & 3)) * 32 + r32] = y;
             }
         }
+        if (a.signs) {
+            // gated rows times the signs go back to the same LDS slot (each lane rewrites what it read), for the
+            // rotation below
+            const f4 sg = *reinterpret_cast<const f4*>(a.signs + (int64_t)head * D + dh + 4 * r32);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                f4& yl = xr[(r32 >> 3) * 256 + (2 * i + h) * 8 + (r32 & 7)];
+                f4 y = yl;
+                if (a.gate) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) y[e] = gate_mul_fast(y[e], gz[i][e]);
+                }
+                yl = y * sg;
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int t = t0 + 2 * i + h;
@@ -381,6 +399,31 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         finish(std::integral_constant<int, 0>{});
     else
         finish(std::integral_constant<int, 1>{});
+
+    if (a.signs) {
+        // The block's 32 rows x 2 blocks of 512 (heads 2j, 2j+1 of this kv head) are rotated by one wave each,
+        // 8 per wave: row 4 wave + k/2, block k%2. Element p = lane + 64 e of block j is head 2j + e/4, dim
+        // lane + 64 (e%4), finished by group (e/2)%2: its value sits in that group's slot of that head
+        // (group 0: lds_s1, group 1: lds_s0) at float ((dim%128)/32) * 1024 + row * 32 + dim % 32.
+        __syncthreads();
+#pragma unroll 1
+        for (int k = 0; k < 8; k++) {
+            const int r = 4 * wave + (k >> 1), j = k & 1, t = t0 + r;
+            if (t >= a.T) break;  // rows are in order: the rest are past the end too
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float* slot = reinterpret_cast<const float*>((((e >> 1) & 1) ? lds_s0 : lds_s1) +
+                                                                   (2 * j + (e >> 2)) * PF_XSLOT);
+                const int dd = lane + 64 * (e & 1);
+                v[e] = slot[(dd >> 5) * 1024 + r * 32 + (dd & 31)];
+            }
+            fwht512_wave(v, lane);
+            float* o = a.out + (int64_t)t * a.o_ts + (int64_t)(kh * 4 + 2 * j) * a.o_hs;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[(e >> 2) * a.o_hs + lane + 64 * (e & 3)] = v[e] * INV_SQRT512;
+        }
+    }
 }
 
 }  // namespace bn

@@ -86,8 +86,8 @@ typedef struct bn_attn_args {
     const float* signs; /* [H * 256] +1/-1 (16-byte aligned), or NULL. When set, `out` receives o_proj's input
                            instead of the gated output: the rest of gate_rotate (gate_rotate.comp:22-25), i.e.
                            per row and block of 512 elements (heads 2j, 2j+1), H_512 (gated * signs) / sqrt(512).
-                           Decode and verify calls rotate in their epilogue; prefill calls rotate in place after
-                           the attention kernel. */
+                           The attention kernels rotate in their epilogue (the fallback prefill kernel for
+                           calls too small to fill the GPU rotates in place after it). */
 } bn_attn_args;
 
 #define BN_Q_F16 1u
