@@ -30,6 +30,8 @@ struct bn_ctx {
     int decode_waves;
     // waves a decode launch aims at (256 .. BN_DECODE_MAX_TARGET_WAVES; BONSAI_ATTN_DECODE_TARGET_WAVES)
     int decode_target_waves;
+    // splits of one sequence at most (1 .. kMaxSplitsCap; BONSAI_ATTN_DECODE_MAX_SPLITS)
+    int decode_max_splits;
     char err[256];
 };
 
@@ -60,22 +62,29 @@ int64_t ceil_div(int64_t x, int64_t m) { return (x + m - 1) / m; }
 #ifndef BN_DECODE_WAVES
 #define BN_DECODE_WAVES 2
 #endif
+#ifndef BN_DECODE_MAX_SPLITS
+#define BN_DECODE_MAX_SPLITS 64
+#endif
+// the workspace query sizes the partials without a cap on the splits of one sequence
+constexpr int64_t kMaxSplitsCap = 1 << 20;
 
 // Single-token decodes: about `target_waves` waves over the launch in blocks of W waves, i.e.
 // target = target_waves / (W KV) splits per kv head, of equal length over the whole batch (the
-// kernels derive the chunk from the device-side lengths with bn::dec_chunk). A launch is `units` blocks wide
+// kernels derive the chunk from the device-side lengths with bn::dec_chunk), and no more than max_splits splits
+// for one sequence (the merge of one sequence runs on two blocks per kv head, so a long single sequence cut
+// into hundreds of splits would wait on its merge: 95 us against 27 us for 16K keys with the cap at 64). A launch is `units` blocks wide
 // per kv head, an upper bound of the splits: sum_i ceil(L_i / chunk) <= sum_i L_i / chunk + nseq <=
 // target + nseq, and no sequence takes more than ceil(max_len / 64) splits. The workspace query has no
 // context, so it sizes the partials for W = 1 and BN_DECODE_MAX_TARGET_WAVES, the most splits a context gives.
 struct DecodePlan {
-    int64_t nseq, KV, max_len, target, units, waves;
+    int64_t nseq, KV, max_len, target, max_splits, units, waves;
     bool multi;  // some sequence may take more than one split (then the partials need the workspace)
     size_t part_bytes;
     size_t total() const { return multi ? part_bytes : 0; }
 };
 
 DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len, int64_t known_len, int64_t waves,
-                       int64_t target_waves) {
+                       int64_t target_waves, int64_t max_splits) {
     DecodePlan p;
     p.nseq = nseq;
     p.KV = KV;
@@ -83,9 +92,10 @@ DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len, int64_t known_
     p.waves = waves;
     p.target = target_waves / (waves * KV);
     if (p.target < 1) p.target = 1;
+    p.max_splits = max_splits;
     if (known_len >= 0) {
         // one sequence of known length: the exact split count
-        const int64_t chunk = bn::dec_chunk(known_len, (int)p.target, (int)max_len);
+        const int64_t chunk = bn::dec_chunk(known_len, (int)p.target, (int)max_len, (int)p.max_splits);
         p.units = known_len > 0 ? ceil_div(known_len, chunk) : 1;
         p.multi = p.units > 1;
     } else {
@@ -100,12 +110,12 @@ DecodePlan plan_decode(int64_t nseq, int64_t KV, int64_t max_len, int64_t known_
 
 // T query rows of one sequence run as T single-token decodes: row t attends to off + t + 1 keys (causal among the
 // rows). The lengths are known on the host, so the split count is exact.
-DecodePlan plan_rows(const bn_attn_args* a, int64_t waves, int64_t target_waves) {
+DecodePlan plan_rows(const bn_attn_args* a, int64_t waves, int64_t target_waves, int64_t max_splits) {
     const int64_t T = a->T, off = a->off;
-    DecodePlan p = plan_decode(T, a->KV, off + T, T == 1 ? off + 1 : -1, waves, target_waves);
+    DecodePlan p = plan_decode(T, a->KV, off + T, T == 1 ? off + 1 : -1, waves, target_waves, max_splits);
     if (T > 1) {
         const int64_t sum = T * (off + 1) + T * (T - 1) / 2;
-        const int64_t chunk = bn::dec_chunk(sum, (int)p.target, (int)(off + T));
+        const int64_t chunk = bn::dec_chunk(sum, (int)p.target, (int)(off + T), (int)p.max_splits);
         p.units = 0;
         for (int64_t t = 0; t < T; t++) p.units += ceil_div(off + 1 + t, chunk);
         p.multi = p.units > T;
@@ -309,7 +319,7 @@ bn_status launch_decode(bn_ctx* ctx, hipStream_t st, const bn::DecodeArgs& d, co
     }
     bn_status s = launched(ctx, "decode_split_kernel");
     if (s || !p.multi) return s;
-    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3((unsigned)p.nseq, (unsigned)p.KV), dim3(256), 0, st, d);
+    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3((unsigned)p.nseq, (unsigned)(2 * p.KV)), dim3(512), 0, st, d);
     return launched(ctx, "decode_combine_kernel");
 }
 
@@ -317,6 +327,7 @@ void bind_workspace(bn::DecodeArgs& d, const DecodePlan& p, void* ws) {
     d.nseq = (int)p.nseq;
     d.max_len = (int)p.max_len;
     d.target = (int)p.target;
+    d.max_splits = (int)p.max_splits;
     d.units = (int)p.units;
     d.part = p.multi ? static_cast<float*>(ws) : nullptr;
 }
@@ -325,7 +336,7 @@ void bind_workspace(bn::DecodeArgs& d, const DecodePlan& p, void* ws) {
 // fuses its append into the split kernel (the new row is its last key); several rows append first, since row t
 // reads the new rows before it from the cache.
 bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
-    DecodePlan p = plan_rows(a, ctx->decode_waves, ctx->decode_target_waves);
+    DecodePlan p = plan_rows(a, ctx->decode_waves, ctx->decode_target_waves, ctx->decode_max_splits);
     const bool fused = a->T == 1;
     if (!fused && a->k_new) {
         bn_status s = launch_append(ctx, st, a);
@@ -538,6 +549,11 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
         const int v = atoi(e);
         if (v >= 256 && v <= BN_DECODE_MAX_TARGET_WAVES) c->decode_target_waves = v;
     }
+    c->decode_max_splits = BN_DECODE_MAX_SPLITS;
+    if (const char* e = getenv("BONSAI_ATTN_DECODE_MAX_SPLITS")) {
+        const int v = atoi(e);
+        if (v >= 1 && v <= kMaxSplitsCap) c->decode_max_splits = v;
+    }
     if (const char* e = getenv("BONSAI_ATTN_FLASH2_MIN_BLOCKS")) {
         const int v = atoi(e);
         if (v >= 1) c->flash2_min_blocks = v;
@@ -553,7 +569,7 @@ const char* bn_ctx_last_error(const bn_ctx* ctx) { return ctx ? ctx->err : g_che
 
 size_t bn_attn_workspace_size(const bn_attn_args* a) {
     if (!a || a->KV < 1 || a->T < 1) return 0;
-    const size_t rows = a->T <= (uint32_t)kVerifyMax ? plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES).total() : 0;
+    const size_t rows = a->T <= (uint32_t)kVerifyMax ? plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap).total() : 0;
     if (a->T == 1) return rows;
     // the kernel choice for T >= 2 depends on the context, so the size covers both families
     const size_t f2 = a->T >= (uint32_t)bn::F2_BQ ? plan_flash2(a->T, a->off, a->KV).total() : 0;
@@ -564,7 +580,7 @@ size_t bn_attn_workspace_size(const bn_attn_args* a) {
 
 size_t bn_ragged_workspace_size(const bn_ragged_args* a) {
     if (!a || a->KV < 1 || a->nseq < 1 || a->max_len < 1) return 0;
-    return plan_decode(a->nseq, a->KV, a->max_len, -1, 1, BN_DECODE_MAX_TARGET_WAVES).total();
+    return plan_decode(a->nseq, a->KV, a->max_len, -1, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap).total();
 }
 
 bn_status bn_attn_check(const bn_attn_args* a, int kind) { return check_attn(a, kind, g_check_err); }
@@ -623,7 +639,8 @@ bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_a
     if (!ctx) return BN_EINVAL;
     bn_status s = check_ragged(a, ctx->err);
     if (s) return s;
-    DecodePlan p = plan_decode(a->nseq, a->KV, a->max_len, -1, ctx->decode_waves, ctx->decode_target_waves);
+    DecodePlan p = plan_decode(a->nseq, a->KV, a->max_len, -1, ctx->decode_waves, ctx->decode_target_waves,
+                               ctx->decode_max_splits);
     bn::DecodeArgs d{};
     d.q = a->q;
     d.q_ss = a->q_ss;

@@ -21,9 +21,11 @@
 //   PV: fp32 FMAs on the VALU; each lane owns 8 dims of every other key and the 4 heads.
 //   Combine: a sequence that fits one split is finished (divided and gated) by its split. Otherwise each
 //   split writes (m, l, acc[256]) per head to the workspace and decode_combine_kernel, launched next on the
-//   same stream, merges them in split order and gates. The kernel boundary makes the partials visible
-//   across the XCDs' separate L2s; a device-scope fence per block (an L2 write-back plus invalidate on
-//   gfx950) would cost far more. The merge order is fixed, so results do not depend on scheduling.
+//   same stream, merges them (four waves per head, each over every fourth split, then the four sums in wave
+//   order) and gates. The kernel boundary makes the partials visible across the XCDs' separate L2s; a
+//   device-scope fence per block (an L2 write-back plus invalidate on gfx950) costs far more (measured: the
+//   8K x 32 decode took 284 us with a last-block merge against 176 us with the second launch). The merge order
+//   is fixed, so results do not depend on scheduling.
 //   Append: when k_new/v_new are given, the new row (last key of the sequence) is taken from them, rounded
 //   to fp16, used for the score and the PV product, and stored into the cache by the same split.
 #pragma once
@@ -55,14 +57,19 @@ struct DecodeArgs {
     float* part;         // [KV][units][DEC_PART]
     int KV, nseq, max_len;
     int target;          // splits aimed at per kv head
+    int max_splits;      // splits of one sequence at most
     int units;           // launch width per kv head (>= sum_i n_i)
 };
 
 constexpr int DEC_MIN_CHUNK = 64;
 
-// Keys per split for a batch with `sum_len` keys in total (per kv head); the same on host and device.
-__host__ __device__ inline int dec_chunk(int64_t sum_len, int target, int max_len) {
+// Keys per split for a batch with `sum_len` keys in total (per kv head): about sum_len / target, at least
+// DEC_MIN_CHUNK, and enough that no sequence (of at most max_len keys) takes more than max_splits splits; the
+// same on host and device.
+__host__ __device__ inline int dec_chunk(int64_t sum_len, int target, int max_len, int max_splits) {
     int64_t c = (sum_len + target - 1) / target;
+    const int64_t cs = ((int64_t)max_len + max_splits - 1) / max_splits;
+    if (c < cs) c = cs;
     c = (c + 15) / 16 * 16;
     if (c < DEC_MIN_CHUNK) c = DEC_MIN_CHUNK;
     const int64_t cap = ((int64_t)max_len + 15) / 16 * 16;
@@ -103,7 +110,7 @@ __device__ DecSplit dec_find_unit(const DecodeArgs& a, int b, int lane) {
     const int L0 = lane < a.nseq ? dec_len(a, lane) : 0;  // the first 64 lengths stay in registers
     int64_t tot = L0;
     for (int base = 64; base < a.nseq; base += 64) tot += base + lane < a.nseq ? dec_len(a, base + lane) : 0;
-    r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len);
+    r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len, a.max_splits);
     r.seq = -1;
     r.P = r.n = r.L = 0;
     int prefix = 0;
@@ -132,7 +139,7 @@ __device__ DecSplit dec_find_seq(const DecodeArgs& a, int seq, int lane) {
     const int L0 = lane < a.nseq ? dec_len(a, lane) : 0;
     int64_t tot = L0;
     for (int base = 64; base < a.nseq; base += 64) tot += base + lane < a.nseq ? dec_len(a, base + lane) : 0;
-    r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len);
+    r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len, a.max_splits);
     r.seq = seq;
     int prefix = 0;
     for (int base = 0; base <= seq; base += 64) {
@@ -442,49 +449,54 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
     }
 }
 
-// Merge of the split partials of one (sequence, kv head): M = max m_s, L = sum l_s 2^(m_s - M),
-// out = (sum acc_s 2^(m_s - M)) / L (attn_combine.comp:10-20), then the gate and, with signs, the rotation
-// (gate_rotate.comp:18-25: waves 0 and 1 each transform one 512-element block of the group). The accumulators are summed in
-// split order; the m/l terms are reduced across the wave in a fixed order, so results are reproducible.
-// Runs as its own launch after decode_split_kernel, so the partials are visible without device-wide fences.
-// Block = 4 waves per (sequence, kv head), wave = query head; lane: dims 4*lane .. +3, and split
-// base + lane for the m/l terms.
-__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
-    __shared__ float rot_lds[4 * D];  // the group's gated rows times the signs, when the output is rotated
-    const int seq = blockIdx.x, kh = blockIdx.y;
-    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, d0 = lane * 4;
+// Merge of the split partials of one (sequence, kv head, head pair j): for each head M = max m_s,
+// L = sum l_s 2^(m_s - M), out = (sum acc_s 2^(m_s - M)) / L (attn_combine.comp:10-20), then the gate and, with
+// signs, the rotation of the pair's 512 elements (gate_rotate.comp:18-25). Block = 8 waves: waves 4i .. 4i+3
+// merge head 2j + i, wave q of them the splits q, q + 4, q + 8, ... (lane: dims 4 lane .. +3, and one split per
+// lane for the m/l terms); each wave sums its splits in order, and the four sums are added in LDS in wave order,
+// so results are reproducible. Runs as its own launch after decode_split_kernel, so the partials are visible
+// without device-wide fences. Grid (sequences, 2 KV).
+__global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
+    __shared__ f4 o_lds[8][64];
+    __shared__ float m_lds[8], l_lds[8];
+    __shared__ float y_lds[2 * D];  // the pair's gated rows times the signs, when the output is rotated
+    const int seq = blockIdx.x, kh = blockIdx.y >> 1, j = blockIdx.y & 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i = wave >> 2, q = wave & 3, d0 = lane * 4;
     const DecSplit sp = dec_find_seq(a, seq, lane);
     const int ns = sp.n;
     if (ns <= 1) return;  // written by the split kernel
-    const int head = kh * 4 + h;
-    f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.gate) z = *reinterpret_cast<const f4*>(a.gate + seq * a.g_ss + head * a.g_hs + d0);
-    const float* pb = a.part + ((int64_t)kh * a.units + sp.P) * DEC_PART;
+    const int h = 2 * j + i, head = kh * 4 + h;
+    const float* pb = a.part + ((int64_t)kh * a.units + sp.P + q) * DEC_PART;  // this wave's first split
     const float* pa = pb + 8 + h * D + d0;
-    // the first 16 splits' accumulators are requested before anything waits, together with the m terms
-    constexpr int PRE = 16;
+    constexpr int64_t STEP = 4 * DEC_PART;  // to the wave's next split
+    const int nk = (ns - q + 3) >> 2;        // splits q, q + 4, ... below ns
+    // the first accumulators are requested before anything waits, together with the m terms
+    constexpr int PRE = 8;
     f4 pre[PRE];
 #pragma unroll
     for (int u = 0; u < PRE; u++)
-        pre[u] = u < ns ? *reinterpret_cast<const f4*>(pa + (int64_t)u * DEC_PART) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        pre[u] = u < nk ? *reinterpret_cast<const f4*>(pa + u * STEP) : f4{0.0f, 0.0f, 0.0f, 0.0f};
     float M = -INFINITY;
-    for (int s = lane; s < ns; s += 64) M = fmaxf(M, pb[(int64_t)s * DEC_PART + h]);
+    for (int k = lane; k < nk; k += 64) M = fmaxf(M, pb[k * STEP + h]);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
+    if (lane == 0) m_lds[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(m_lds[4 * i], m_lds[4 * i + 1]), fmaxf(m_lds[4 * i + 2], m_lds[4 * i + 3]));
     float Ls = 0.0f;
     f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int base = 0; base < ns; base += 64) {
-        const int s = base + lane;
+    for (int base = 0; base < nk; base += 64) {
+        const int k = base + lane;
         float w = 0.0f, lw = 0.0f;
-        if (s < ns) {
-            const float ms = pb[(int64_t)s * DEC_PART + h];
+        if (k < nk) {
+            const float ms = pb[k * STEP + h];
             w = ms == -INFINITY ? 0.0f : exp2f(ms - M);
-            lw = pb[(int64_t)s * DEC_PART + 4 + h] * w;
+            lw = pb[k * STEP + 4 + h] * w;
         }
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) lw += __shfl_xor(lw, m);
         Ls += lw;
-        const int cnt = min(64, ns - base);
+        const int cnt = min(64, nk - base);
         int j0 = 0;
         if (base == 0) {
 #pragma unroll
@@ -501,7 +513,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
             f4 v[8];
 #pragma unroll
             for (int u = 0; u < 8; u++)
-                if (j0 + u < cnt) v[u] = *reinterpret_cast<const f4*>(pa + (int64_t)(base + j0 + u) * DEC_PART);
+                if (j0 + u < cnt) v[u] = *reinterpret_cast<const f4*>(pa + (int64_t)(base + j0 + u) * STEP);
 #pragma unroll
             for (int u = 0; u < 8; u++)
                 if (j0 + u < cnt) {
@@ -511,19 +523,30 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
                 }
         }
     }
-    f4 y;
+    o_lds[wave][lane] = o;
+    if (lane == 0) l_lds[wave] = Ls;
+    __syncthreads();
+    if (q == 0) {  // wave 4i finishes head 2j + i
+        const f4 s = ((o_lds[wave][lane] + o_lds[wave + 1][lane]) + o_lds[wave + 2][lane]) + o_lds[wave + 3][lane];
+        const float L = ((l_lds[wave] + l_lds[wave + 1]) + l_lds[wave + 2]) + l_lds[wave + 3];
+        f4 y;
+        if (a.gate) {
+            const f4 z = *reinterpret_cast<const f4*>(a.gate + seq * a.g_ss + head * a.g_hs + d0);
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        y[e] = o[e] / Ls;
-        if (a.gate) y[e] = gate_mul(y[e], z[e]);
+            for (int e = 0; e < 4; e++) y[e] = gate_mul(s[e] / L, z[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = s[e] / L;
+        }
+        if (a.signs)
+            *reinterpret_cast<f4*>(&y_lds[i * D + d0]) = y * *reinterpret_cast<const f4*>(a.signs + head * D + d0);
+        else
+            *reinterpret_cast<f4*>(a.out + seq * a.o_ss + head * a.o_hs + d0) = y;
     }
     if (a.signs) {
-        *reinterpret_cast<f4*>(&rot_lds[h * D + d0]) = y * *reinterpret_cast<const f4*>(a.signs + head * D + d0);
         __syncthreads();
-        if (h < 2) rotate_group_store(rot_lds, a.out + seq * a.o_ss + (int64_t)kh * 4 * a.o_hs, a.o_hs, h, lane);
-        return;
+        if (wave == 0) rotate_pair_store(y_lds, a.out + seq * a.o_ss + (int64_t)(kh * 4 + 2 * j) * a.o_hs, a.o_hs, lane);
     }
-    *reinterpret_cast<f4*>(a.out + seq * a.o_ss + head * a.o_hs + d0) = y;
 }
 
 }  // namespace bn

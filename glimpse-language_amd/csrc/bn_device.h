@@ -118,16 +118,20 @@ __device__ __forceinline__ void fwht512_wave(float (&v)[8], int lane) {
 
 constexpr float INV_SQRT512 = 0.044194173824159216f;
 
-// The rotated output of one (row, kv head) group: `lds` holds y[h*256 + d] * sign for the group's 4 heads; the
-// calling wave transforms 512-element block j (heads 2j, 2j+1) and stores it at o (the group's head 0) with head
-// stride o_hs. All 64 lanes take part.
-__device__ __forceinline__ void rotate_group_store(const float* lds, float* o, int64_t o_hs, int j, int lane) {
+// The rotated output of one head pair: `lds` holds y[i*256 + d] * sign for heads 2j + i (i = 0, 1); the calling
+// wave transforms the 512 elements and stores them at o (head 2j) with head stride o_hs. All 64 lanes take part.
+__device__ __forceinline__ void rotate_pair_store(const float* lds, float* o, int64_t o_hs, int lane) {
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) v[e] = lds[j * 512 + lane + 64 * e];
+    for (int e = 0; e < 8; e++) v[e] = lds[lane + 64 * e];
     fwht512_wave(v, lane);
 #pragma unroll
-    for (int e = 0; e < 8; e++) o[(2 * j + (e >> 2)) * o_hs + lane + 64 * (e & 3)] = v[e] * INV_SQRT512;
+    for (int e = 0; e < 8; e++) o[(e >> 2) * o_hs + lane + 64 * (e & 3)] = v[e] * INV_SQRT512;
+}
+
+// The same for block j of one (row, kv head) group: `lds` holds the group's 4 heads, o is the group's head 0.
+__device__ __forceinline__ void rotate_group_store(const float* lds, float* o, int64_t o_hs, int j, int lane) {
+    rotate_pair_store(lds + j * 512, o + 2 * j * o_hs, o_hs, lane);
 }
 
 }  // namespace bn
