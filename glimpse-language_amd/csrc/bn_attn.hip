@@ -255,7 +255,6 @@ bn_status check_prep(const bn_prep_args* a, char* why) {
     if (!a) return set_err(why, BN_EINVAL, "args is NULL");
     if (a->KV < 1 || a->H != 4 * a->KV)
         return set_err(why, BN_EINVAL, "need H == 4*KV >= 4 (H=%u KV=%u)", a->H, a->KV);
-    if (a->H + 2 * a->KV > 4u * 65535u) return set_err(why, BN_EINVAL, "too many heads (H=%u)", a->H);
     if (a->T < 1) return set_err(why, BN_EINVAL, "T must be >= 1");
     if ((uint64_t)a->off + a->T > a->cap)
         return set_err(why, BN_EINVAL, "off + T = %llu exceeds cap = %u", (unsigned long long)a->off + a->T, a->cap);
@@ -283,10 +282,11 @@ bn_status check_rotate(const bn_rotate_args* a, char* why) {
     if (a->H < 2 || (a->H & 1) || a->H > 2u * 65535u)
         return set_err(why, BN_EINVAL, "H must be even, 2..131070 (H=%u)", a->H);
     if (!a->attn || !a->signs || !a->xr) return set_err(why, BN_EINVAL, "attn, signs and xr are required");
-    if (((uintptr_t)a->attn & 3) || ((uintptr_t)a->signs & 3) || ((uintptr_t)a->xr & 3) || ((uintptr_t)a->gate & 3))
-        return set_err(why, BN_EINVAL, "attn, gate, signs and xr must be 4-byte aligned");
-    if (a->a_ts < 0 || a->x_ts < 0 || (a->gate && (a->g_ts < 0 || a->g_hs < 0)))
-        return set_err(why, BN_EINVAL, "strides must be non-negative");
+    if (!aligned16(a->attn) || !aligned16(a->signs) || !aligned16(a->xr) || !aligned16(a->gate))
+        return set_err(why, BN_EINVAL, "attn, gate, signs and xr must be 16-byte aligned");
+    if (a->a_ts < 0 || a->x_ts < 0 || (a->a_ts & 3) || (a->x_ts & 3) ||
+        (a->gate && (a->g_ts < 0 || a->g_hs < 0 || (a->g_ts & 3) || (a->g_hs & 3))))
+        return set_err(why, BN_EINVAL, "strides must be non-negative multiples of 4 elements");
     if ((const float*)a->xr == a->attn && a->x_ts != a->a_ts)
         return set_err(why, BN_EINVAL, "xr may be attn itself only with the same stride");
     return BN_OK;
@@ -697,8 +697,7 @@ bn_status bn_attn_prep(bn_ctx* ctx, bn_stream stream, const bn_prep_args* a) {
     p.rot = (int)a->rot;
     p.s1 = (int)a->s1;
     p.s2 = (int)a->s2;
-    const dim3 grid(a->T, (unsigned)ceil_div(a->H + 2 * a->KV, 4));
-    hipLaunchKernelGGL(bn::prep_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(bn::prep_kernel, dim3(a->T), dim3(256), 0, (hipStream_t)stream, p);
     return launched(ctx, "prep_kernel");
 }
 

@@ -70,14 +70,16 @@ __device__ __forceinline__ float dpp_f32(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
-// Unnormalised 512-point Walsh-Hadamard transform of v held by one wave: lane l holds elements l + 64 e
-// (e = 0..7). Index bits 0-5 are butterflies across lanes, bits 6-8 inside the lane; the stages commute, so the
-// result is H_512 v (common.glsl:55-72 fwht512 computes the same transform with 32-lane subgroups and 16 elements
-// per lane). A cross-lane butterfly pairs lane l with l ^ m: the lower lane needs own + partner, the upper one
-// partner - own. Every lane computes own + s partner instead (s = -1 on the upper lane), which leaves the upper
-// lane's result negated; the two lanes of a later stage have taken the same sides so far, so they carry the same
-// sign, and the signs are settled once at the end: (-1)^popcount(l). The partners come from DPP moves (m = 1, 2,
-// 4 = 7 then 3, 8) and v_permlane16/32_swap (m = 16, 32), with no LDS traffic.
+// Unnormalised 512-point Walsh-Hadamard transform of v held by one wave: 6 index bits are lane bits, 3 are bits
+// of e (v[e], e = 0..7); which index bits they are is the caller's mapping (the callers here use element
+// 256 (e/4) + 4 lane + e%4, so a lane's values are two 16-byte groups). H_512 is the tensor product of H_2 over
+// the 9 bits, so any such mapping and any stage order give H_512 v (common.glsl:55-72 fwht512 computes the same
+// transform with 32-lane subgroups and 16 elements per lane). A cross-lane butterfly pairs lane l with l ^ m:
+// the lower lane needs own + partner, the upper one partner - own. Every lane computes own + s partner instead
+// (s = -1 on the upper lane), which leaves the upper lane's result negated; the two lanes of a later stage have
+// taken the same sides so far, so they carry the same sign, and the signs are settled once at the end:
+// (-1)^popcount(l). The partners come from DPP moves (m = 1, 2, 4 = 7 then 3, 8) and v_permlane16/32_swap
+// (m = 16, 32), with no LDS traffic.
 __device__ __forceinline__ void fwht512_wave(float (&v)[8], int lane) {
     const float s1 = (lane & 1) ? -1.0f : 1.0f, s2 = (lane & 2) ? -1.0f : 1.0f, s4 = (lane & 4) ? -1.0f : 1.0f;
     const float s8 = (lane & 8) ? -1.0f : 1.0f, s16 = (lane & 16) ? -1.0f : 1.0f, s32 = (lane & 32) ? -1.0f : 1.0f;
@@ -119,14 +121,21 @@ __device__ __forceinline__ void fwht512_wave(float (&v)[8], int lane) {
 constexpr float INV_SQRT512 = 0.044194173824159216f;
 
 // The rotated output of one head pair: `lds` holds y[i*256 + d] * sign for heads 2j + i (i = 0, 1); the calling
-// wave transforms the 512 elements and stores them at o (head 2j) with head stride o_hs. All 64 lanes take part.
+// wave transforms the 512 elements and stores them at o (head 2j) with head stride o_hs (a multiple of 4, o
+// 16-byte aligned). All 64 lanes take part.
 __device__ __forceinline__ void rotate_pair_store(const float* lds, float* o, int64_t o_hs, int lane) {
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) v[e] = lds[lane + 64 * e];
+    for (int i = 0; i < 2; i++) {
+        const f4 x = *reinterpret_cast<const f4*>(lds + 256 * i + 4 * lane);
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[4 * i + c] = x[c];
+    }
     fwht512_wave(v, lane);
 #pragma unroll
-    for (int e = 0; e < 8; e++) o[(e >> 2) * o_hs + lane + 64 * (e & 3)] = v[e] * INV_SQRT512;
+    for (int i = 0; i < 2; i++)
+        *reinterpret_cast<f4*>(o + i * o_hs + 4 * lane) =
+            f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512;
 }
 
 // The same for block j of one (row, kv head) group: `lds` holds the group's 4 heads, o is the group's head 0.

@@ -402,26 +402,31 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 
     if (a.signs) {
         // The block's 32 rows x 2 blocks of 512 (heads 2j, 2j+1 of this kv head) are rotated by one wave each,
-        // 8 per wave: row 4 wave + k/2, block k%2. Element p = lane + 64 e of block j is head 2j + e/4, dim
-        // lane + 64 (e%4), finished by group (e/2)%2: its value sits in that group's slot of that head
-        // (group 0: lds_s1, group 1: lds_s0) at float ((dim%128)/32) * 1024 + row * 32 + dim % 32.
+        // 8 per wave: row 4 wave + k/2, block k%2. Lane l holds dims 4l .. 4l+3 of heads 2j and 2j+1 (the
+        // mapping of rotate_pair_store); dim 4l + c was finished by group l/32: its value sits in that group's
+        // slot of that head (group 0: lds_s1, group 1: lds_s0) at float ((dim%128)/32) * 1024 + row * 32 +
+        // dim % 32, so a lane's four dims are one 16-byte read.
         __syncthreads();
+        const int dd = 4 * (lane & 31);
+        const uint8_t* gslot = lane < 32 ? lds_s1 : lds_s0;
 #pragma unroll 1
         for (int k = 0; k < 8; k++) {
             const int r = 4 * wave + (k >> 1), j = k & 1, t = t0 + r;
             if (t >= a.T) break;  // rows are in order: the rest are past the end too
             float v[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float* slot = reinterpret_cast<const float*>((((e >> 1) & 1) ? lds_s0 : lds_s1) +
-                                                                   (2 * j + (e >> 2)) * PF_XSLOT);
-                const int dd = lane + 64 * (e & 1);
-                v[e] = slot[(dd >> 5) * 1024 + r * 32 + (dd & 31)];
+            for (int i = 0; i < 2; i++) {
+                const float* slot = reinterpret_cast<const float*>(gslot + (2 * j + i) * PF_XSLOT);
+                const f4 x = *reinterpret_cast<const f4*>(slot + (dd >> 5) * 1024 + r * 32 + (dd & 31));
+#pragma unroll
+                for (int c = 0; c < 4; c++) v[4 * i + c] = x[c];
             }
             fwht512_wave(v, lane);
             float* o = a.out + (int64_t)t * a.o_ts + (int64_t)(kh * 4 + 2 * j) * a.o_hs;
 #pragma unroll
-            for (int e = 0; e < 8; e++) o[(e >> 2) * a.o_hs + lane + 64 * (e & 3)] = v[e] * INV_SQRT512;
+            for (int i = 0; i < 2; i++)
+                *reinterpret_cast<f4*>(o + i * a.o_hs + 4 * lane) =
+                    f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512;
         }
     }
 }

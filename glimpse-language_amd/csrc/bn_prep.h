@@ -26,34 +26,46 @@ struct PrepArgs {
     int T, off, H, KV, rot, s1, s2;
 };
 
-// Grid (T, ceil((H + 2 KV) / 4)) x 4 waves; wave = one head row: q heads [0, H), k heads [H, H+KV), v heads
-// [H+KV, H+2KV). Lane l holds dims 4l .. 4l+3.
-//   q/k: x * (1 / sqrt(sum x^2 / 256 + 1e-6)) * w (a wave-wide sum), then on dims d < rot (pairs d, d + rot/2;
-//   pair index i = d mod rot/2): position row sel = 1 if i % 3 == 1 and i < 3 s1, 2 if i % 3 == 2 and i < 3 s2,
-//   else 0; angle pos[sel][t] * inv_freq[i]; x' = x cos - x[d + rot/2] sin (first half), x cos + x[d - rot/2]
-//   sin (second half). The partner element is held by lane l +- rot/8.
+// Token t's rotation of lane l's dims 4l .. 4l+3 (d < rot; pairs d, d + rot/2, pair index i = d mod rot/2):
+// position row sel = 1 if i % 3 == 1 and i < 3 s1, 2 if i % 3 == 2 and i < 3 s2, else 0 (attn_prep.comp:51);
+// angle pos[sel][t] * inv_freq[i] in fp32. The same for every q and k head of the token.
+__device__ __forceinline__ void prep_angles(const PrepArgs& a, int t, int d0, f4& cs, f4& sn) {
+    const int half = a.rot >> 1;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        cs[e] = 1.0f;
+        sn[e] = 0.0f;
+    }
+    if (d0 >= a.rot) return;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = (d0 + e) % half;
+        const int sel = (i % 3 == 1 && i < 3 * a.s1) ? 1 : ((i % 3 == 2 && i < 3 * a.s2) ? 2 : 0);
+        const float ang = (float)a.pos[sel * a.T + t] * a.inv_freq[i];
+        float s_, c_;
+        sincosf(ang, &s_, &c_);
+        sn[e] = s_;
+        cs[e] = c_;
+    }
+}
+
+// One head row of token t: q heads [0, H), k heads [H, H+KV), v heads [H+KV, H+2KV); lane l holds dims
+// 4l .. 4l+3 (x, already loaded; w the norm weights of those dims, cs/sn the token's rotation).
+//   q/k: x * (1 / sqrt(sum x^2 / 256 + 1e-6)) * w (a wave-wide sum), then on dims d < rot:
+//   x' = x cos - x[d + rot/2] sin (first half), x cos + x[d - rot/2] sin (second half); the partner element is
+//   held by lane l +- rot/8.
 //   v: copied. k and v are rounded to fp16 (nearest even) into cache row off + t.
-__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
-    const int t = blockIdx.x, lane = threadIdx.x & 63;
-    const int hh = blockIdx.y * 4 + (threadIdx.x >> 6);
+__device__ __forceinline__ void prep_row(const PrepArgs& a, int t, int hh, f4 x, f4 w, f4 cs, f4 sn, int lane) {
     const int H = a.H, KV = a.KV, d0 = 4 * lane;
-    if (hh >= H + 2 * KV) return;
-    const int64_t kvd = (int64_t)KV * D;
     if (hh >= H + KV) {
-        const int kh = hh - H - KV;
-        const f4 v = *reinterpret_cast<const f4*>(a.vp + t * kvd + kh * D + d0);
-        const h4 y = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-        *reinterpret_cast<h4*>(a.vc + ((int64_t)(a.off + t) * KV + kh) * D + d0) = y;
+        const h4 y = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+        *reinterpret_cast<h4*>(a.vc + ((int64_t)(a.off + t) * KV + (hh - H - KV)) * D + d0) = y;
         return;
     }
-    const bool isq = hh < H;
-    f4 x = isq ? *reinterpret_cast<const f4*>(a.qp + t * a.qp_ts + hh * a.qp_hs + d0)
-               : *reinterpret_cast<const f4*>(a.kp + t * kvd + (hh - H) * D + d0);
     float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
     const float r = 1.0f / sqrtf(ss / 256.0f + 1e-6f);
-    const f4 w = *reinterpret_cast<const f4*>((isq ? a.qn : a.kn) + d0);
 #pragma unroll
     for (int e = 0; e < 4; e++) x[e] = x[e] * r * w[e];
     const int half = a.rot >> 1;
@@ -65,16 +77,9 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++) xp[e] = __shfl(x[e], pl);
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int d = d0 + e, i = d % half;
-            const int sel = (i % 3 == 1 && i < 3 * a.s1) ? 1 : ((i % 3 == 2 && i < 3 * a.s2) ? 2 : 0);
-            const float ang = (float)a.pos[sel * a.T + t] * a.inv_freq[i];
-            float sn, cs;
-            sincosf(ang, &sn, &cs);
-            x[e] = d < half ? x[e] * cs - xp[e] * sn : x[e] * cs + xp[e] * sn;
-        }
+        for (int e = 0; e < 4; e++) x[e] = d0 < half ? x[e] * cs[e] - xp[e] * sn[e] : x[e] * cs[e] + xp[e] * sn[e];
     }
-    if (isq) {
+    if (hh < H) {
         if (a.q16) {
             const h4 y = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
             *reinterpret_cast<h4*>(a.q16 + t * a.q_ts + hh * a.q_hs + d0) = y;
@@ -84,6 +89,39 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     } else {
         const h4 y = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
         *reinterpret_cast<h4*>(a.kc + ((int64_t)(a.off + t) * KV + (hh - H)) * D + d0) = y;
+    }
+}
+
+constexpr int PREP_B = 4;  // head rows per wave with their loads in flight together
+
+// Grid (T) x 4 waves: block = token t; wave w takes head rows w, w + 4, w + 8, ..., PREP_B of them at a time with
+// all their loads issued before the first is used (one row per wave left too few bytes in flight per CU to
+// reach the HBM rate). The norm weights and the token's sin/cos are fetched once per wave, before the rows.
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
+    const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.H, KV = a.KV, nh = H + 2 * KV, d0 = 4 * lane;
+    const int64_t kvd = (int64_t)KV * D;
+    const f4 wq = *reinterpret_cast<const f4*>(a.qn + d0);
+    const f4 wk = *reinterpret_cast<const f4*>(a.kn + d0);
+    f4 cs, sn;
+    prep_angles(a, t, d0, cs, sn);
+    for (int h0 = wave; h0 < nh; h0 += 4 * PREP_B) {
+        f4 x[PREP_B];
+#pragma unroll
+        for (int b = 0; b < PREP_B; b++) {
+            const int hh = h0 + 4 * b;
+            if (hh < H)
+                x[b] = *reinterpret_cast<const f4*>(a.qp + t * a.qp_ts + hh * a.qp_hs + d0);
+            else if (hh < H + KV)
+                x[b] = *reinterpret_cast<const f4*>(a.kp + t * kvd + (hh - H) * D + d0);
+            else if (hh < nh)
+                x[b] = *reinterpret_cast<const f4*>(a.vp + t * kvd + (hh - H - KV) * D + d0);
+        }
+#pragma unroll
+        for (int b = 0; b < PREP_B; b++) {
+            const int hh = h0 + 4 * b;
+            if (hh < nh) prep_row(a, t, hh, x[b], hh < H ? wq : wk, cs, sn, lane);
+        }
     }
 }
 
@@ -98,24 +136,30 @@ struct RotateArgs {
     int T, W;                // W = H * 256, a multiple of 512
 };
 
-// Grid (T, W / 512) x one wave: block b of token t is elements 512b .. 512b+511 (two heads). Lane l holds elements
-// l + 64e (e = 0..7): v = attn * sigmoid(gate) * sign, then the unnormalised Walsh-Hadamard transform
-// (fwht512_wave), then x 1/sqrt(512).
+// Grid (T, W / 512) x one wave: block b of token t is elements 512b .. 512b+511 (heads 2b, 2b+1). Lane l holds
+// elements 256 i + 4 l + c (i = 0, 1; c = 0..3) as v[4 i + c], loaded 16 bytes at a time: v = attn *
+// sigmoid(gate) * sign, then the unnormalised Walsh-Hadamard transform (fwht512_wave), then x 1/sqrt(512).
 __global__ __launch_bounds__(64) void rotate_kernel(RotateArgs a) {
-    const int t = blockIdx.x, b0 = blockIdx.y * 512, lane = threadIdx.x;
+    const int t = blockIdx.x, lane = threadIdx.x;
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int i = b0 + lane + 64 * e, hd = i >> 8, d = i & 255;
-        const float at = a.attn[t * a.a_ts + hd * a.a_hs + d];
-        v[e] = (a.gate ? gate_mul(at, a.gate[t * a.g_ts + hd * a.g_hs + d]) : at) * a.signs[i];
+    for (int i = 0; i < 2; i++) {
+        const int hd = 2 * blockIdx.y + i, d = 4 * lane;
+        f4 x = *reinterpret_cast<const f4*>(a.attn + t * a.a_ts + hd * a.a_hs + d);
+        if (a.gate) {
+            const f4 z = *reinterpret_cast<const f4*>(a.gate + t * a.g_ts + hd * a.g_hs + d);
+#pragma unroll
+            for (int c = 0; c < 4; c++) x[c] = gate_mul(x[c], z[c]);
+        }
+        x *= *reinterpret_cast<const f4*>(a.signs + hd * D + d);
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[4 * i + c] = x[c];
     }
     fwht512_wave(v, lane);
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int i = b0 + lane + 64 * e;
-        a.xr[t * a.x_ts + (i >> 8) * a.x_hs + (i & 255)] = v[e] * INV_SQRT512;
-    }
+    for (int i = 0; i < 2; i++)
+        *reinterpret_cast<f4*>(a.xr + t * a.x_ts + (2 * blockIdx.y + i) * a.x_hs + 4 * lane) =
+            f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512;
 }
 
 }  // namespace bn

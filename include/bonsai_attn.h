@@ -148,7 +148,7 @@ typedef struct bn_prep_args {
  *   v[e] = attn[e] * sigmoid(gate[h][d]) * signs[e],   xr = H_512 v / sqrt(512)
  * with H_512 the Walsh-Hadamard matrix (common.glsl:55-72 fwht512). With gate == NULL attn is taken as already
  * gated (bn_attn_forward with a gate). */
-typedef struct bn_rotate_args {
+typedef struct bn_rotate_args {   /* pointers 16-byte aligned, strides multiples of 4 elements */
     uint32_t T, H;               /* rows and heads; H even (W = 256 H elements per row) */
     const float* attn;           /* element t*a_ts + e */
     int64_t a_ts;
