@@ -42,3 +42,19 @@ def gpu():
     yield torch, ctx, ws
     torch.cuda.synchronize()
     ctx.close()
+
+
+def context_with(**env):
+    """A bn_ctx on device 0 created with the given BONSAI_ATTN_* environment variables set (the context reads
+    its knobs once, at creation); the environment is restored afterwards."""
+    from glimpse_language_amd import bonsai_attn as ba
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return ba.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v

@@ -5,13 +5,12 @@ blocks as the GPU has CUs (for example the 4096-row prefill); here a second cont
 BONSAI_ATTN_PREFILL_MIN_BLOCKS=1 sends every T >= 2 call there, so small shapes cover its tails, offsets,
 head counts, the merge of an empty or partly empty second half, and its rescale path.
 """
-import os
-
 import numpy as np
 import pytest
 
 import oracle
 import workload
+from conftest import context_with
 from test_gpu_attn import assert_parity, cache_np, to_dev
 from glimpse_language_amd import bonsai_attn as ba
 
@@ -21,15 +20,7 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(scope="module")
 def pf(gpu):
     torch, _, _ = gpu
-    old = os.environ.get("BONSAI_ATTN_PREFILL_MIN_BLOCKS")
-    os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"] = "1"
-    try:
-        ctx = ba.Context(0)
-    finally:
-        if old is None:
-            del os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"]
-        else:
-            os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"] = old
+    ctx = context_with(BONSAI_ATTN_PREFILL_MIN_BLOCKS=1)
     ws = ba.Workspace(ctx, "cuda")
     yield torch, ctx, ws
     torch.cuda.synchronize()

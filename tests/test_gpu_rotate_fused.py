@@ -7,15 +7,15 @@ Checked two ways on every case:
   - against the oracle: oracle attention, then oracle gate_rotate with the gate logits set to +inf (sigmoid = 1
     exactly, so the oracle rotates its already-gated output): max-abs 2e-3 and the same projected argmax.
 Cases cover each kernel that can finish a row: the decode split kernel (one split), the split merge (many
-splits), verify rows, the prefill kernels (rotated in place after them) and ragged batches.
+splits), verify rows, prefill_kernel (in its epilogue), flash_kernel (rotated in place after it) and ragged
+batches.
 """
-import os
-
 import numpy as np
 import pytest
 
 import oracle
 import workload
+from conftest import context_with
 from test_gpu_attn import assert_parity, make_ragged, to_dev
 from glimpse_language_amd import bonsai_attn as ba
 
@@ -67,19 +67,12 @@ def test_forward_flash_rotated(gpu):
     check_rotated(gpu, workload.layer(0x9300, T=100, off=700, H=8, KV=2), ba.KIND_FORWARD)
 
 
-def test_prefill_kernel_rotated(gpu):
-    torch, _, _ = gpu
-    old = os.environ.get("BONSAI_ATTN_PREFILL_MIN_BLOCKS")
-    os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"] = "1"
-    try:
-        ctx = ba.Context(0)
-    finally:
-        if old is None:
-            del os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"]
-        else:
-            os.environ["BONSAI_ATTN_PREFILL_MIN_BLOCKS"] = old
+@pytest.mark.parametrize("T,off", [(96, 200), (45, 0)])
+def test_prefill_kernel_rotated(gpu, T, off):
+    torch = gpu[0]
+    ctx = context_with(BONSAI_ATTN_PREFILL_MIN_BLOCKS=1)
     ws = ba.Workspace(ctx, "cuda")
-    check_rotated((torch, ctx, ws), workload.layer(0x9400, T=96, off=200, H=8, KV=2), ba.KIND_PREFILL)
+    check_rotated((torch, ctx, ws), workload.layer(0x9400 + T, T=T, off=off, H=8, KV=2), ba.KIND_PREFILL)
     torch.cuda.synchronize()
     ctx.close()
 
