@@ -11,7 +11,6 @@
 
 #include "bn_decode.h"
 #include "bn_flash.h"
-#include "bn_flash2.h"
 #include "bn_prefill.h"
 #include "bn_prep.h"
 #include "bn_util_kernels.h"
@@ -19,10 +18,6 @@
 struct bn_ctx {
     int device;
     int cus;
-    // T >= 64 calls use flash2_kernel when they give at least this many 64-token q-tile blocks (default: never,
-    // until it beats flash_kernel; the environment variable BONSAI_ATTN_FLASH2_MIN_BLOCKS overrides it at
-    // context creation, e.g. 1 to run every T >= 64 call through flash2_kernel in tests)
-    int flash2_min_blocks;
     // T >= 2 calls use prefill_kernel when they give at least this many 32-token q-tile blocks (default: the
     // CU count; BONSAI_ATTN_PREFILL_MIN_BLOCKS overrides it at context creation, e.g. 1 in tests)
     int prefill_min_blocks;
@@ -155,12 +150,6 @@ FlashPlan plan_flash(int64_t T, int64_t off, int64_t KV) {
     return p;
 }
 
-// T >= 64 rows with enough 64-token q-tiles to fill the GPU: flash2_kernel (64 rows per wave). Depends only on
-// the shapes.
-bool use_flash2(int64_t T, int64_t KV, int64_t min_blocks) {
-    return T >= bn::F2_BQ && KV * ceil_div(T, bn::F2_BQ) >= min_blocks;
-}
-
 // T >= 2 rows with enough 32-token q-tiles to fill the GPU: prefill_kernel (one block per q-tile, the key range
 // split between the block's two wave groups). Depends only on the shapes and the context's threshold.
 // The kernel reads the gate 16 bytes at a time, so a gate pointer or strides that are not whole 16-byte groups
@@ -168,24 +157,6 @@ bool use_flash2(int64_t T, int64_t KV, int64_t min_blocks) {
 bool use_prefill(const bn_attn_args* a, int64_t min_blocks) {
     if (a->gate && (!aligned16(a->gate) || (a->g_ts & 3) || (a->g_hs & 3))) return false;
     return a->T >= 2 && (int64_t)a->KV * ceil_div(a->T, bn::PF_BQ) >= min_blocks;
-}
-
-struct Flash2Plan {
-    int64_t ntq, ct, max_splits;
-    size_t acc_bytes, ml_bytes;
-    size_t total() const { return max_splits > 1 ? acc_bytes + ml_bytes : 0; }
-};
-
-Flash2Plan plan_flash2(int64_t T, int64_t off, int64_t KV) {
-    Flash2Plan p;
-    p.ntq = ceil_div(T, bn::F2_BQ);
-    const int64_t max_kt = ceil_div(off + T, bn::F2_BK);
-    p.ct = max_kt;
-    p.max_splits = 1;
-    const int64_t rows = KV * p.ntq * p.max_splits * bn::F2_ROWS;
-    p.acc_bytes = (size_t)rows * bn::D * sizeof(float);
-    p.ml_bytes = (size_t)rows * 2 * sizeof(float);
-    return p;
 }
 
 bn_status check_attn(const bn_attn_args* a, int kind, char* why) {
@@ -370,41 +341,6 @@ bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     return launch_decode(ctx, st, d, p);
 }
 
-bn_status run_flash2(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
-    Flash2Plan p = plan_flash2(a->T, a->off, a->KV);
-    bn::Flash2Args f{};
-    if (a->flags & BN_Q_F16)
-        f.q16 = static_cast<const uint16_t*>(a->q);
-    else
-        f.q = static_cast<const float*>(a->q);
-    f.q_ts = a->q_ts;
-    f.q_hs = a->q_hs;
-    f.kc = a->kc;
-    f.vc = a->vc;
-    f.gate = a->gate;
-    f.g_ts = a->g_ts;
-    f.g_hs = a->g_hs;
-    f.out = a->out;
-    f.o_ts = a->o_ts;
-    f.o_hs = a->o_hs;
-    f.T = (int)a->T;
-    f.off = (int)a->off;
-    f.KV = (int)a->KV;
-    f.ntq = (int)p.ntq;
-    f.ct = (int)p.ct;
-    f.max_splits = (int)p.max_splits;
-    if (p.max_splits > 1) {
-        f.part_acc = static_cast<float*>(a->ws);
-        f.part_ml = reinterpret_cast<float*>(static_cast<char*>(a->ws) + p.acc_bytes);
-    }
-    const int64_t blocks = (int64_t)a->KV * p.ntq * p.max_splits;
-    hipLaunchKernelGGL(bn::flash2_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
-    bn_status s = launched(ctx, "flash2_kernel");
-    if (s || p.max_splits == 1) return s;
-    hipLaunchKernelGGL(bn::flash2_combine_kernel, dim3(a->T, a->H), dim3(64), 0, st, f);
-    return launched(ctx, "flash2_combine_kernel");
-}
-
 bn_status run_prefill(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     bn::PrefillArgs f{};
     if (a->flags & BN_Q_F16)
@@ -438,7 +374,6 @@ bn_status attend_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
         if (s) return s;
     }
     if (use_prefill(a, ctx->prefill_min_blocks)) return run_prefill(ctx, st, a);
-    if (use_flash2(a->T, a->KV, ctx->flash2_min_blocks)) return run_flash2(ctx, st, a);
     FlashPlan p = plan_flash(a->T, a->off, a->KV);
     bn::FlashArgs f{};
     if (a->flags & BN_Q_F16)
@@ -473,8 +408,8 @@ bn_status attend_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     return launched(ctx, "flash_combine_kernel");
 }
 
-// The rotation of the gated output in place, after flash_kernel / flash2_kernel (the decode kernels and
-// prefill_kernel rotate in their own epilogue).
+// The rotation of the gated output in place, after flash_kernel (the decode kernels and prefill_kernel rotate in
+// their own epilogue).
 bn_status rotate_in_place(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     bn::RotateArgs r{};
     r.attn = a->out;
@@ -533,7 +468,6 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
     if (!c) return BN_EDEVICE;
     c->device = device;
     c->cus = prop.multiProcessorCount;
-    c->flash2_min_blocks = 1 << 30;
     c->prefill_min_blocks = c->cus;
     if (const char* e = getenv("BONSAI_ATTN_PREFILL_MIN_BLOCKS")) {
         const int v = atoi(e);
@@ -554,10 +488,6 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
         const int v = atoi(e);
         if (v >= 1 && v <= kMaxSplitsCap) c->decode_max_splits = v;
     }
-    if (const char* e = getenv("BONSAI_ATTN_FLASH2_MIN_BLOCKS")) {
-        const int v = atoi(e);
-        if (v >= 1) c->flash2_min_blocks = v;
-    }
     c->err[0] = 0;
     *out = c;
     return BN_OK;
@@ -571,10 +501,8 @@ size_t bn_attn_workspace_size(const bn_attn_args* a) {
     if (!a || a->KV < 1 || a->T < 1) return 0;
     const size_t rows = a->T <= (uint32_t)kVerifyMax ? plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap).total() : 0;
     if (a->T == 1) return rows;
-    // the kernel choice for T >= 2 depends on the context, so the size covers both families
-    const size_t f2 = a->T >= (uint32_t)bn::F2_BQ ? plan_flash2(a->T, a->off, a->KV).total() : 0;
-    const size_t f1 = plan_flash(a->T, a->off, a->KV).total();
-    const size_t fl = f1 > f2 ? f1 : f2;
+    // the kernel choice for T >= 2 depends on the context, so the size covers the flash kernel's partials
+    const size_t fl = plan_flash(a->T, a->off, a->KV).total();
     return fl > rows ? fl : rows;
 }
 
