@@ -191,6 +191,40 @@ class Workloads:
         return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
 
+    def layer(self, steps, warmup, H, KV, T, off, seed=0xB0A5A108):
+        """bn_attn_layer: attn_prep + attention + gate + rotation in one call, from raw q_proj / k_proj / v_proj
+        rows (q_proj's output [T][H][512], its second half the gate logits)."""
+        torch, ba, ctx = self.torch, self.ba, self.ctx
+        g = self._gen(seed)
+        cap = off + T
+        kc = rms(torch, torch.randn(cap, KV, D, device="cuda", generator=g)).half().view(torch.int16)
+        vc = torch.randn(cap, KV, D, device="cuda", generator=g).half().view(torch.int16)
+        qp = torch.randn(T, H, 512, device="cuda", generator=g)
+        kp = torch.randn(T, KV, D, device="cuda", generator=g)
+        vp = torch.randn(T, KV, D, device="cuda", generator=g)
+        qn = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+        kn = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+        p = torch.arange(off, off + T, device="cuda", dtype=torch.int32)
+        pos = torch.stack([p, p, p]).contiguous()
+        inv = 1.0 / (1e7 ** (torch.arange(32, device="cuda", dtype=torch.float32) * 2 / 64))
+        signs = self.signs(H)
+        out = torch.empty(T, H, D, device="cuda")
+        # a prefill's q goes through an fp16 scratch (BN_Q_F16), the form prefill_kernel reads fastest
+        q = torch.empty(T, H, D, device="cuda", dtype=torch.float16) if T > ba.VERIFY_MAX else None
+
+        def step():
+            ba.attention_layer(ctx, self.ws, qp, kp, vp, qn, kn, pos, inv, kc, vc, off, gate=qp[:, :, D:],
+                               signs=signs, out=out, q=q)
+
+        ms, wall = time_steps(torch, step, steps, warmup)
+        flops = attn_flops(H, T, off)
+        # cache rows read once (fp16), q half and gate half of q_proj, out, k/v rows in (fp32) and fp16 rows out
+        nbytes = (off * KV * D * 2 * 2 + T * H * D * (4 + 4 + 4) + T * KV * D * 2 * (4 + 2) + T * KV * D * 2 * 2
+                  + H * D * 4)
+        return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12, bytes=nbytes,
+                    gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
+
+
 def measured_traffic(name):
     """HBM bytes per step from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ (its
     `traffic_bytes_per_step:` line), or (None, None) when the summary is absent."""
@@ -243,7 +277,7 @@ def cpu_baseline(budget_s=10.0, H=16, KV=4, L=8192, nseq=2):
 
 ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix",
        "decode_8k_batch32_rotated", "prefill_4k_rotated", "verify_8_rotated", "prep_4k", "prep_decode",
-       "gate_rotate_4k")
+       "gate_rotate_4k", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k")
 
 
 def main():
@@ -324,6 +358,18 @@ def main():
         log("gate_rotate_4k")
         res["gate_rotate_4k"] = r = W.rotate(K, Wm, 16, 4096)
         log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "layer_decode_8k" in only:
+        log("layer_decode_8k")
+        res["layer_decode_8k"] = r = W.layer(K, Wm, 16, 4, 1, 8191)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "layer_verify_8" in only:
+        log("layer_verify_8")
+        res["layer_verify_8"] = r = W.layer(K, Wm, 16, 4, 8, 8184)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "layer_prefill_4k" in only:
+        log("layer_prefill_4k")
+        res["layer_prefill_4k"] = r = W.layer(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0)
+        log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")

@@ -25,7 +25,7 @@ EXPORTS = (
     "bn_attn_workspace_size", "bn_ragged_workspace_size", "bn_attn_check", "bn_ragged_check",
     "bn_workspace_clear", "bn_attn_forward", "bn_attn_decode", "bn_attn_verify", "bn_attn_prefill",
     "bn_attn_append", "bn_attn_decode_ragged", "bn_prep_check", "bn_rotate_check", "bn_attn_prep",
-    "bn_gate_rotate",
+    "bn_gate_rotate", "bn_attn_layer",
 )
 
 
@@ -126,6 +126,8 @@ def load(path=LIB_PATH):
     lib.bn_attn_prep.restype = ctypes.c_int
     lib.bn_gate_rotate.argtypes = [P, P, ctypes.POINTER(RotateArgs)]
     lib.bn_gate_rotate.restype = ctypes.c_int
+    lib.bn_attn_layer.argtypes = [P, P, ctypes.POINTER(PrepArgs), ctypes.POINTER(AttnArgs)]
+    lib.bn_attn_layer.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -358,3 +360,39 @@ def gate_rotate(ctx, attn, signs, gate=None, xr=None, stream=None):
         xr = torch.empty((attn.shape[0], signs.numel()), dtype=torch.float32, device=attn.device)
     ctx.call("bn_gate_rotate", rotate_args(attn, signs, xr, gate), stream)
     return xr
+
+
+def attention_layer(ctx, ws, qp, kp, vp, q_norm, k_norm, pos, inv_freq, kc, vc, off, gate=None, signs=None,
+                    out=None, q=None, rot=64, s1=11, s2=11, stream=None):
+    """bn_attn_layer: attn_prep + attention (+ gate, + rotation with signs) in one call. qp [T, H, >=256] raw q
+    rows (q_proj's output as it is), kp/vp [T, KV, 256] raw; gate a [T, H, 256] view with unit stride in the
+    last dim (e.g. qp[:, :, 256:]); q: scratch [T, H, 256] for T > 16 (allocated when None)."""
+    import torch
+    T, H = qp.shape[0], qp.shape[1]
+    KV, cap = kc.shape[1], kc.shape[0]
+    if out is None:
+        out = torch.empty((T, H, D), dtype=torch.float32, device=qp.device)
+    if q is None and T > VERIFY_MAX:
+        q = torch.empty((T, H, D), dtype=torch.float32, device=qp.device)
+    p = PrepArgs()
+    p.T, p.off, p.H, p.KV, p.cap = T, off, H, KV, cap
+    p.flags = BN_Q_F16 if (q is not None and q.dtype == torch.float16) else 0
+    p.rot, p.s1, p.s2 = rot, s1, s2
+    p.qp, p.qp_ts, p.qp_hs = _ptr(qp), qp.stride(0), qp.stride(1)
+    p.kp, p.vp, p.q_norm, p.k_norm = _ptr(kp), _ptr(vp), _ptr(q_norm), _ptr(k_norm)
+    p.pos, p.inv_freq = _ptr(pos), _ptr(inv_freq)
+    p.q = _ptr(q)
+    p.q_ts, p.q_hs = (q.stride(0), q.stride(1)) if q is not None else (0, 0)
+    p.kc, p.vc = _ptr(kc), _ptr(vc)
+    g_strides = (gate.stride(0), gate.stride(1)) if gate is not None else None
+    a = attn_args(T, off, H, KV, cap, None, kc, vc, out, None, None, gate, None, 0, (0, 0), g_strides, None,
+                  signs=signs)
+    probe = attn_args(T, off, H, KV, cap, qp, kc, vc, out, kp, vp, gate, None, 0, (qp.stride(0), qp.stride(1)),
+                      g_strides, None, signs=signs)
+    need = workspace_size(probe)
+    buf = ws.get(need) if ws is not None else None
+    a.ws = _ptr(buf)
+    a.ws_bytes = 0 if buf is None else buf.numel()
+    st = ctx.lib.bn_attn_layer(ctx.h, ctx._stream(stream), ctypes.byref(p), ctypes.byref(a))
+    ctx._check(st, "bn_attn_layer")
+    return out

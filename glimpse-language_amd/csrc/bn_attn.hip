@@ -74,6 +74,7 @@ constexpr int64_t kMaxSplitsCap = 1 << 20;
 struct DecodePlan {
     int64_t nseq, KV, max_len, target, max_splits, units, waves;
     bool multi;  // some sequence may take more than one split (then the partials need the workspace)
+    bool xcd_rows = false;  // rows of one sequence in the XCD-aware unit order (bn::DecodeArgs::xcd_rows)
     size_t part_bytes;
     size_t total() const { return multi ? part_bytes : 0; }
 };
@@ -109,11 +110,14 @@ DecodePlan plan_rows(const bn_attn_args* a, int64_t waves, int64_t target_waves,
     const int64_t T = a->T, off = a->off;
     DecodePlan p = plan_decode(T, a->KV, off + T, T == 1 ? off + 1 : -1, waves, target_waves, max_splits);
     if (T > 1) {
+        // every row reads the same cache rows: split s of all rows goes to one XCD (units 8 (t + T (s / 8)) +
+        // s % 8), so each split's K/V rows come from HBM once and from that XCD's L2 for the other rows
         const int64_t sum = T * (off + 1) + T * (T - 1) / 2;
         const int64_t chunk = bn::dec_chunk(sum, (int)p.target, (int)(off + T), (int)p.max_splits);
-        p.units = 0;
-        for (int64_t t = 0; t < T; t++) p.units += ceil_div(off + 1 + t, chunk);
-        p.multi = p.units > T;
+        const int64_t ns_max = ceil_div(off + T, chunk);
+        p.xcd_rows = true;
+        p.units = 8 * T * ceil_div(ns_max, 8);
+        p.multi = ns_max > 1;
         p.part_bytes = (size_t)(a->KV * p.units) * bn::DEC_PART * sizeof(float);
     }
     return p;
@@ -222,7 +226,7 @@ bn_status check_ragged(const bn_ragged_args* a, char* why) {
     return BN_OK;
 }
 
-bn_status check_prep(const bn_prep_args* a, char* why) {
+bn_status check_prep(const bn_prep_args* a, char* why, bool q_optional = false) {
     if (!a) return set_err(why, BN_EINVAL, "args is NULL");
     if (a->KV < 1 || a->H != 4 * a->KV)
         return set_err(why, BN_EINVAL, "need H == 4*KV >= 4 (H=%u KV=%u)", a->H, a->KV);
@@ -233,7 +237,7 @@ bn_status check_prep(const bn_prep_args* a, char* why) {
     if (a->flags & ~BN_Q_F16) return set_err(why, BN_EINVAL, "unknown flags 0x%x", a->flags);
     if ((a->rot & 7) || a->rot > (uint32_t)bn::D)
         return set_err(why, BN_EINVAL, "rot must be a multiple of 8 in 0..256 (rot=%u)", a->rot);
-    if (!a->qp || !a->kp || !a->vp || !a->q_norm || !a->k_norm || !a->q || !a->kc || !a->vc)
+    if (!a->qp || !a->kp || !a->vp || !a->q_norm || !a->k_norm || (!a->q && !q_optional) || !a->kc || !a->vc)
         return set_err(why, BN_EINVAL, "qp, kp, vp, q_norm, k_norm, q, kc and vc are required");
     if (a->rot && (!a->pos || !a->inv_freq)) return set_err(why, BN_EINVAL, "pos and inv_freq are required when rot > 0");
     if (!aligned16(a->qp) || !aligned16(a->kp) || !aligned16(a->vp) || !aligned16(a->q_norm) ||
@@ -283,7 +287,12 @@ bn_status launch_decode(bn_ctx* ctx, hipStream_t st, const bn::DecodeArgs& d, co
     const dim3 grid((unsigned)p.units, (unsigned)p.KV);
     switch (p.waves) {
         case 1: hipLaunchKernelGGL(bn::decode_split_kernel<1>, grid, dim3(64), 0, st, d); break;
-        case 2: hipLaunchKernelGGL(bn::decode_split_kernel<2>, grid, dim3(128), 0, st, d); break;
+        case 2:
+            if (p.xcd_rows)
+                hipLaunchKernelGGL((bn::decode_split_kernel<2, true>), grid, dim3(128), 0, st, d);
+            else
+                hipLaunchKernelGGL((bn::decode_split_kernel<2, false>), grid, dim3(128), 0, st, d);
+            break;
         case 4: hipLaunchKernelGGL(bn::decode_split_kernel<4>, grid, dim3(256), 0, st, d); break;
         case 8: hipLaunchKernelGGL(bn::decode_split_kernel<8>, grid, dim3(512), 0, st, d); break;
         default: hipLaunchKernelGGL(bn::decode_split_kernel<16>, grid, dim3(1024), 0, st, d); break;
@@ -300,13 +309,16 @@ void bind_workspace(bn::DecodeArgs& d, const DecodePlan& p, void* ws) {
     d.target = (int)p.target;
     d.max_splits = (int)p.max_splits;
     d.units = (int)p.units;
+    d.xcd_rows = p.xcd_rows;
     d.part = p.multi ? static_cast<float*>(ws) : nullptr;
 }
 
 // Query rows as single-token decodes (row t over off + t + 1 keys, the sequence's rows at stride q_ts). One row
 // fuses its append into the split kernel (the new row is its last key); several rows append first, since row t
 // reads the new rows before it from the cache.
-bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+// rp (optional): attn_prep in the kernels' prologue; a->q and, for one row, a->k_new are then raw q_proj / k_proj
+// rows (several rows have their K/V rows written by prep_kernel before this call).
+bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, const bn::RopeParams* rp = nullptr) {
     DecodePlan p = plan_rows(a, ctx->decode_waves, ctx->decode_target_waves, ctx->decode_max_splits);
     const bool fused = a->T == 1;
     if (!fused && a->k_new) {
@@ -336,6 +348,7 @@ bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     d.o_ss = a->o_ts;
     d.o_hs = a->o_hs;
     d.signs = a->signs;
+    if (rp) d.rp = *rp;
     d.KV = (int)a->KV;
     bind_workspace(d, p, a->ws);
     return launch_decode(ctx, st, d, p);
@@ -430,6 +443,61 @@ bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     bn_status s = attend_flash(ctx, st, a);
     if (s || !a->signs || fused) return s;
     return rotate_in_place(ctx, st, a);
+}
+
+// prep_kernel over the rows of p; kv_only: K/V cache rows only (the attention kernel norms and rotates q itself)
+bn_status launch_prep(bn_ctx* ctx, hipStream_t st, const bn_prep_args* a, bool kv_only) {
+    bn::PrepArgs p{};
+    p.qp = a->qp;
+    p.qp_ts = a->qp_ts;
+    p.qp_hs = a->qp_hs;
+    p.kp = a->kp;
+    p.vp = a->vp;
+    p.rp.qn = a->q_norm;
+    p.rp.kn = a->k_norm;
+    p.rp.pos = a->pos;
+    p.rp.inv_freq = a->inv_freq;
+    p.rp.npos = (int)a->T;
+    p.rp.rot = (int)a->rot;
+    p.rp.s1 = (int)a->s1;
+    p.rp.s2 = (int)a->s2;
+    if (!kv_only) {
+        if (a->flags & BN_Q_F16)
+            p.q16 = static_cast<uint16_t*>(a->q);
+        else
+            p.q = static_cast<float*>(a->q);
+    }
+    p.q_ts = a->q_ts;
+    p.q_hs = a->q_hs;
+    p.kc = a->kc;
+    p.vc = a->vc;
+    p.T = (int)a->T;
+    p.off = (int)a->off;
+    p.H = (int)a->H;
+    p.KV = (int)a->KV;
+    hipLaunchKernelGGL(bn::prep_kernel, dim3(a->T), dim3(256), 0, st, p);
+    return launched(ctx, "prep_kernel");
+}
+
+// bn_attn_layer's arguments: p's checks (its q output needed only for more than kVerifyMax rows), a's q, k_new
+// and v_new NULL, the same rows in both, and a's checks with p's raw rows in place of q, k_new and v_new (m).
+bn_status check_layer(const bn_prep_args* p, const bn_attn_args* a, bn_attn_args* m, char* why) {
+    if (!p || !a) return set_err(why, BN_EINVAL, "args is NULL");
+    bn_status s = check_prep(p, why, p->T <= (uint32_t)kVerifyMax);
+    if (s) return s;
+    if (a->q || a->k_new || a->v_new)
+        return set_err(why, BN_EINVAL, "q, k_new and v_new of the attention args must be NULL (the rows come from prep)");
+    if (a->flags) return set_err(why, BN_EINVAL, "attention flags must be 0 (q's form is prep's flags)");
+    if (p->T != a->T || p->off != a->off || p->H != a->H || p->KV != a->KV || p->cap != a->cap || p->kc != a->kc ||
+        p->vc != a->vc)
+        return set_err(why, BN_EINVAL, "prep and attention args describe different rows or caches");
+    *m = *a;
+    m->q = p->qp;
+    m->q_ts = p->qp_ts;
+    m->q_hs = p->qp_hs;
+    m->k_new = p->kp;
+    m->v_new = p->vp;
+    return check_attn(m, 0, why);
 }
 
 // kind: 0 forward, 1 decode, 2 verify, 3 prefill. One row is always a decode; verify-sized calls (T <= 16) of the
@@ -600,33 +668,47 @@ bn_status bn_attn_prep(bn_ctx* ctx, bn_stream stream, const bn_prep_args* a) {
     if (!ctx) return BN_EINVAL;
     bn_status s = check_prep(a, ctx->err);
     if (s) return s;
-    bn::PrepArgs p{};
-    p.qp = a->qp;
-    p.qp_ts = a->qp_ts;
-    p.qp_hs = a->qp_hs;
-    p.kp = a->kp;
-    p.vp = a->vp;
-    p.qn = a->q_norm;
-    p.kn = a->k_norm;
-    p.pos = a->pos;
-    p.inv_freq = a->inv_freq;
-    if (a->flags & BN_Q_F16)
-        p.q16 = static_cast<uint16_t*>(a->q);
-    else
-        p.q = static_cast<float*>(a->q);
-    p.q_ts = a->q_ts;
-    p.q_hs = a->q_hs;
-    p.kc = a->kc;
-    p.vc = a->vc;
-    p.T = (int)a->T;
-    p.off = (int)a->off;
-    p.H = (int)a->H;
-    p.KV = (int)a->KV;
-    p.rot = (int)a->rot;
-    p.s1 = (int)a->s1;
-    p.s2 = (int)a->s2;
-    hipLaunchKernelGGL(bn::prep_kernel, dim3(a->T), dim3(256), 0, (hipStream_t)stream, p);
-    return launched(ctx, "prep_kernel");
+    return launch_prep(ctx, (hipStream_t)stream, a, false);
+}
+
+bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, const bn_attn_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_attn_args m;
+    bn_status s = check_layer(p, a, &m, ctx->err);
+    if (s) return s;
+    hipStream_t st = (hipStream_t)stream;
+    bn::RopeParams rp{};
+    rp.qn = p->q_norm;
+    rp.kn = p->k_norm;
+    rp.pos = p->pos;
+    rp.inv_freq = p->inv_freq;
+    rp.npos = (int)p->T;
+    rp.rot = (int)p->rot;
+    rp.s1 = (int)p->s1;
+    rp.s2 = (int)p->s2;
+    if (p->T <= (uint32_t)kVerifyMax) {
+        // decode / verify rows: q normed and rotated in the split kernel's prologue; one row also appends its
+        // K/V row there, several rows have theirs written by prep_kernel first
+        if (p->T > 1) {
+            s = launch_prep(ctx, st, p, true);
+            if (s) return s;
+            m.k_new = nullptr;
+            m.v_new = nullptr;
+        }
+        return run_rows(ctx, st, &m, &rp);
+    }
+    // prefill: prep_kernel writes q (to p->q, fp16 with BN_Q_F16) and the K/V rows, then the prefill kernels read
+    // them (norming q inside prefill_kernel's Q staging was measured slower: 252 against 240 us at 4096 rows,
+    // the staging sits on every block's critical path)
+    s = launch_prep(ctx, st, p, false);
+    if (s) return s;
+    m.k_new = nullptr;
+    m.v_new = nullptr;
+    m.q = p->q;
+    m.q_ts = p->q_ts;
+    m.q_hs = p->q_hs;
+    m.flags = p->flags;
+    return run_flash(ctx, st, &m);
 }
 
 bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a) {

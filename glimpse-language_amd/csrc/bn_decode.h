@@ -30,6 +30,7 @@
 //   to fp16, used for the score and the PV product, and stored into the cache by the same split.
 #pragma once
 #include "bn_device.h"
+#include "bn_prep.h"
 
 namespace bn {
 
@@ -54,11 +55,15 @@ struct DecodeArgs {
     int64_t o_ss, o_hs;
     const float* signs;  // [heads*256] +-1, or null; when set, out receives each row rotated: blocks of 512
                          // (heads 2j, 2j+1) times the signs, Walsh-Hadamard transformed, / sqrt(512)
+    RopeParams rp;       // rp.qn set: q and k_new are raw attn_prep inputs (q_proj rows, k_proj rows) that the
+                         // kernel norms and rotates in its prologue (position column: the sequence index)
     float* part;         // [KV][units][DEC_PART]
     int KV, nseq, max_len;
     int target;          // splits aimed at per kv head
     int max_splits;      // splits of one sequence at most
     int units;           // launch width per kv head (>= sum_i n_i)
+    int xcd_rows;        // rows of one sequence (verify): unit 8 (t + T (s / 8)) + s % 8 is split s of row t, so the
+                         // same split of every row runs on one XCD and shares its K/V rows through that L2
 };
 
 constexpr int DEC_MIN_CHUNK = 64;
@@ -101,8 +106,13 @@ __device__ __forceinline__ int64_t wave_sum64(int64_t x) {
 // The split structure of the batch, as seen from one wave: chunk, and for the sequence found, its first
 // unit P, split count n and length L. Sequences are scanned 64 at a time (one per lane).
 struct DecSplit {
-    int chunk, seq, P, n, L;
+    int chunk, seq, P, n, L, s;  // s: the split of `seq` that the unit works on (dec_find_unit)
 };
+
+// Partial record slot of split s of sequence seq (first unit P).
+__device__ __forceinline__ int dec_slot(const DecodeArgs& a, int P, int seq, int s) {
+    return a.xcd_rows ? 8 * (seq + a.nseq * (s >> 3)) + (s & 7) : P + s;
+}
 
 // Finds the sequence and split that unit `b` works on (seq = -1 when b is past the last split).
 __device__ DecSplit dec_find_unit(const DecodeArgs& a, int b, int lane) {
@@ -112,7 +122,18 @@ __device__ DecSplit dec_find_unit(const DecodeArgs& a, int b, int lane) {
     for (int base = 64; base < a.nseq; base += 64) tot += base + lane < a.nseq ? dec_len(a, base + lane) : 0;
     r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len, a.max_splits);
     r.seq = -1;
-    r.P = r.n = r.L = 0;
+    r.P = r.n = r.L = r.s = 0;
+    if (a.xcd_rows) {
+        const int sb = 8 * (b / (8 * a.nseq)) + (b & 7), t = (b >> 3) % a.nseq;
+        const int L = dec_len(a, t), n = (L + r.chunk - 1) / r.chunk;
+        if (sb < n) {
+            r.seq = t;
+            r.n = n;
+            r.L = L;
+            r.s = sb;
+        }
+        return r;
+    }
     int prefix = 0;
     for (int base = 0; base < a.nseq; base += 64) {
         const int Li = base == 0 ? L0 : (base + lane < a.nseq ? dec_len(a, base + lane) : 0);
@@ -126,6 +147,7 @@ __device__ DecSplit dec_find_unit(const DecodeArgs& a, int b, int lane) {
             r.n = __shfl(n, f);
             r.P = prefix + __shfl(incl, f) - r.n;
             r.L = __shfl(Li, f);
+            r.s = b - r.P;
             break;
         }
         prefix += total;
@@ -141,6 +163,13 @@ __device__ DecSplit dec_find_seq(const DecodeArgs& a, int seq, int lane) {
     for (int base = 64; base < a.nseq; base += 64) tot += base + lane < a.nseq ? dec_len(a, base + lane) : 0;
     r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len, a.max_splits);
     r.seq = seq;
+    r.s = 0;
+    if (a.xcd_rows) {
+        r.L = dec_len(a, seq);
+        r.n = (r.L + r.chunk - 1) / r.chunk;
+        r.P = 0;
+        return r;
+    }
     int prefix = 0;
     for (int base = 0; base <= seq; base += 64) {
         const int Li = base == 0 ? L0 : (base + lane < a.nseq ? dec_len(a, base + lane) : 0);
@@ -168,19 +197,24 @@ __device__ __forceinline__ void wave_lds_sync() {
 // W waves per block. A split's 16-key tiles are dealt to the waves in contiguous runs (wave w: tiles
 // [w nt / W, (w+1) nt / W)); each wave keeps its own online softmax, and the block merges the W partial
 // (m, l, acc) in wave order through LDS. One partial (or the finished output) per block.
-template <int W>
+// SHARED: the K/V rows are read by several units (the rows of one sequence in the XCD-aware order): cached loads,
+// so the other rows find them in L2; otherwise non-temporal loads stream them (a compile-time choice: a branch in
+// the tile loop costs the streaming case 10%).
+template <int W, bool SHARED = false>
 __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
     __shared__ f4 p_lds[W][16];   // per wave: p[key in tile][head]
     __shared__ f4 al_lds[W];      // per wave: per-head rescale of the running accumulators
     __shared__ f4 ml_lds[W][2];   // per wave: final m, l per head
     __shared__ float acc_lds[W > 1 ? W : 1][4 * D];  // per wave: acc[head][dim] (W > 1)
+    __shared__ float q_lds[4 * D];                   // attn_prep in the prologue: the group's q rows
+    __shared__ float k_lds[D];                       // ... and the appended key row
 
     const int b = blockIdx.x, kh = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const int wave = W > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
     const DecSplit sp = dec_find_unit(a, b, lane);
     if (sp.seq < 0) return;
-    const int seq = sp.seq, L = sp.L, ns = sp.n, s = b - sp.P;
+    const int seq = sp.seq, L = sp.L, ns = sp.n, s = sp.s;
     const int64_t row0 = dec_row0(a, seq);
     const int chunk = sp.chunk;
     const int sj0 = s * chunk;
@@ -205,6 +239,25 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[h][e] = 0.0f;
 
+    // attn_prep in the prologue (attn_prep.comp:40-56): the group's 4 q rows (wave w: heads w, w + W, ...) and,
+    // in the wave that appends it, the new key row are normed and rotated into LDS
+    const bool prep = a.rp.qn != nullptr;
+    if (prep) {
+        f4 cs, sn;
+        rope_angles(a.rp, seq, 4 * lane, cs, sn);
+        const f4 wq = *reinterpret_cast<const f4*>(a.rp.qn + 4 * lane);
+        for (int h = wave; h < 4; h += W) {
+            const f4 x = *reinterpret_cast<const f4*>(a.q + seq * a.q_ss + (int64_t)(kh * 4 + h) * a.q_hs + 4 * lane);
+            *reinterpret_cast<f4*>(&q_lds[h * D + 4 * lane]) = norm_rope(x, wq, cs, sn, a.rp.rot, lane);
+        }
+        if (has_new) {
+            const f4 x = *reinterpret_cast<const f4*>(a.k_new + seq * a.kn_ss + kh * D + 4 * lane);
+            const f4 wk = *reinterpret_cast<const f4*>(a.rp.kn + 4 * lane);
+            *reinterpret_cast<f4*>(&k_lds[4 * lane]) = norm_rope(x, wk, cs, sn, a.rp.rot, lane);
+        }
+        __syncthreads();
+    }
+
     if (j0 < j1) {
         // B operand: Q^T, column c = head (c&3), hi part for (c&4)==0 else lo part, k-step ks covers
         // dims ks*32 + g*8 .. +7.
@@ -220,8 +273,9 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
                     for (int e = 0; e < 8; e++) x[e] = (float)v[e];
                 } else {
-                    const f4 u = *reinterpret_cast<const f4*>(a.q + qo + ks * 32);
-                    const f4 v = *reinterpret_cast<const f4*>(a.q + qo + ks * 32 + 4);
+                    const float* qs = prep ? q_lds + (c & 3) * D + g * 8 : a.q + qo;
+                    const f4 u = *reinterpret_cast<const f4*>(qs + ks * 32);
+                    const f4 v = *reinterpret_cast<const f4*>(qs + ks * 32 + 4);
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         x[e] = u[e];
@@ -286,13 +340,13 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
             const int r = min(jt + c, j1 - 1);
             const uint16_t* p = kb + (int64_t)r * kvd + g * 8;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) kt[ks] = ld_h8_nt(p + ks * 32);
+            for (int ks = 0; ks < 8; ks++) kt[ks] = SHARED ? ld_h8(p + ks * 32) : ld_h8_nt(p + ks * 32);
         };
         auto load_v = [&](int jt, h8* vt) {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int r = min(jt + 2 * i + pvr, j1 - 1);
-                vt[i] = ld_h8_nt(vb + (int64_t)r * kvd + pvd);
+                vt[i] = SHARED ? ld_h8(vb + (int64_t)r * kvd + pvd) : ld_h8_nt(vb + (int64_t)r * kvd + pvd);
             }
         };
 
@@ -315,7 +369,7 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
             // row L-1 of the last tile comes from k_new / v_new (fp16, nearest even) and is stored to the
             // cache, so a call that appends and one that finds the row cached produce the same bits
             const int rn = L - 1 - tl;  // tile row of the new key
-            const float* kn = a.k_new + seq * a.kn_ss + kh * D;
+            const float* kn = prep ? k_lds : a.k_new + seq * a.kn_ss + kh * D;
             const float* vn = a.v_new + seq * a.kn_ss + kh * D;
             uint16_t* kdst = a.kc + ((row0 + L - 1) * a.KV + kh) * D;
             uint16_t* vdst = a.vc + ((row0 + L - 1) * a.KV + kh) * D;
@@ -466,18 +520,20 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
     const int ns = sp.n;
     if (ns <= 1) return;  // written by the split kernel
     const int h = 2 * j + i, head = kh * 4 + h;
-    const float* pb = a.part + ((int64_t)kh * a.units + sp.P + q) * DEC_PART;  // this wave's first split
-    const float* pa = pb + 8 + h * D + d0;
-    constexpr int64_t STEP = 4 * DEC_PART;  // to the wave's next split
+    // the record of this wave's k-th split (split q + 4k)
+    auto rec = [&](int k) -> const float* {
+        return a.part + ((int64_t)kh * a.units + dec_slot(a, sp.P, seq, q + 4 * k)) * DEC_PART;
+    };
+    const int ad = 8 + h * D + d0;           // this lane's accumulators in a record
     const int nk = (ns - q + 3) >> 2;        // splits q, q + 4, ... below ns
     // the first accumulators are requested before anything waits, together with the m terms
     constexpr int PRE = 8;
     f4 pre[PRE];
 #pragma unroll
     for (int u = 0; u < PRE; u++)
-        pre[u] = u < nk ? *reinterpret_cast<const f4*>(pa + u * STEP) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        pre[u] = u < nk ? *reinterpret_cast<const f4*>(rec(u) + ad) : f4{0.0f, 0.0f, 0.0f, 0.0f};
     float M = -INFINITY;
-    for (int k = lane; k < nk; k += 64) M = fmaxf(M, pb[k * STEP + h]);
+    for (int k = lane; k < nk; k += 64) M = fmaxf(M, rec(k)[h]);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
     if (lane == 0) m_lds[wave] = M;
@@ -489,9 +545,10 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
         const int k = base + lane;
         float w = 0.0f, lw = 0.0f;
         if (k < nk) {
-            const float ms = pb[k * STEP + h];
+            const float* r = rec(k);
+            const float ms = r[h];
             w = ms == -INFINITY ? 0.0f : exp2f(ms - M);
-            lw = pb[k * STEP + 4 + h] * w;
+            lw = r[4 + h] * w;
         }
 #pragma unroll
         for (int m = 32; m >= 1; m >>= 1) lw += __shfl_xor(lw, m);
@@ -513,7 +570,7 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
             f4 v[8];
 #pragma unroll
             for (int u = 0; u < 8; u++)
-                if (j0 + u < cnt) v[u] = *reinterpret_cast<const f4*>(pa + (int64_t)(base + j0 + u) * STEP);
+                if (j0 + u < cnt) v[u] = *reinterpret_cast<const f4*>(rec(base + j0 + u) + ad);
 #pragma unroll
             for (int u = 0; u < 8; u++)
                 if (j0 + u < cnt) {

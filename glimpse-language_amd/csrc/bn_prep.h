@@ -9,39 +9,32 @@
 
 namespace bn {
 
-struct PrepArgs {
-    const float* qp;         // q rows: element t*qp_ts + h*qp_hs + d (the q half of the q_proj output)
-    int64_t qp_ts, qp_hs;
-    const float* kp;         // [T][KV][256]
-    const float* vp;         // [T][KV][256]
+// The parameters of attn_prep's norm and rotation, shared by prep_kernel and the attention kernels that apply
+// it in their prologue (qn == null: the caller's q and k rows are already normed and rotated).
+struct RopeParams {
     const float* qn;         // [256] q norm weight
     const float* kn;         // [256] k norm weight
-    const int32_t* pos;      // [3][T] mRoPE positions (t, h, w rows)
+    const int32_t* pos;      // [3][npos] mRoPE positions (t, h, w rows); row t of a call is position column t
     const float* inv_freq;   // [rot / 2]
-    float* q;                // element t*q_ts + h*q_hs + d: fp32 ...
-    uint16_t* q16;           // ... or fp16 bits when non-null
-    int64_t q_ts, q_hs;
-    uint16_t* kc;            // fp16 [cap][KV][256]: rows off .. off+T-1 written
-    uint16_t* vc;
-    int T, off, H, KV, rot, s1, s2;
+    int npos, rot, s1, s2;
 };
 
-// Token t's rotation of lane l's dims 4l .. 4l+3 (d < rot; pairs d, d + rot/2, pair index i = d mod rot/2):
-// position row sel = 1 if i % 3 == 1 and i < 3 s1, 2 if i % 3 == 2 and i < 3 s2, else 0 (attn_prep.comp:51);
-// angle pos[sel][t] * inv_freq[i] in fp32. The same for every q and k head of the token.
-__device__ __forceinline__ void prep_angles(const PrepArgs& a, int t, int d0, f4& cs, f4& sn) {
-    const int half = a.rot >> 1;
+// Position column t's rotation of lane l's dims 4l .. 4l+3 (d < rot; pairs d, d + rot/2, pair index
+// i = d mod rot/2): position row sel = 1 if i % 3 == 1 and i < 3 s1, 2 if i % 3 == 2 and i < 3 s2, else 0
+// (attn_prep.comp:51); angle pos[sel][t] * inv_freq[i] in fp32. The same for every q and k head of the token.
+__device__ __forceinline__ void rope_angles(const RopeParams& rp, int t, int d0, f4& cs, f4& sn) {
+    const int half = rp.rot >> 1;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         cs[e] = 1.0f;
         sn[e] = 0.0f;
     }
-    if (d0 >= a.rot) return;
+    if (d0 >= rp.rot) return;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int i = (d0 + e) % half;
-        const int sel = (i % 3 == 1 && i < 3 * a.s1) ? 1 : ((i % 3 == 2 && i < 3 * a.s2) ? 2 : 0);
-        const float ang = (float)a.pos[sel * a.T + t] * a.inv_freq[i];
+        const int sel = (i % 3 == 1 && i < 3 * rp.s1) ? 1 : ((i % 3 == 2 && i < 3 * rp.s2) ? 2 : 0);
+        const float ang = (float)rp.pos[sel * rp.npos + t] * rp.inv_freq[i];
         float s_, c_;
         sincosf(ang, &s_, &c_);
         sn[e] = s_;
@@ -49,29 +42,21 @@ __device__ __forceinline__ void prep_angles(const PrepArgs& a, int t, int d0, f4
     }
 }
 
-// One head row of token t: q heads [0, H), k heads [H, H+KV), v heads [H+KV, H+2KV); lane l holds dims
-// 4l .. 4l+3 (x, already loaded; w the norm weights of those dims, cs/sn the token's rotation).
-//   q/k: x * (1 / sqrt(sum x^2 / 256 + 1e-6)) * w (a wave-wide sum), then on dims d < rot:
-//   x' = x cos - x[d + rot/2] sin (first half), x cos + x[d - rot/2] sin (second half); the partner element is
-//   held by lane l +- rot/8.
-//   v: copied. k and v are rounded to fp16 (nearest even) into cache row off + t.
-__device__ __forceinline__ void prep_row(const PrepArgs& a, int t, int hh, f4 x, f4 w, f4 cs, f4 sn, int lane) {
-    const int H = a.H, KV = a.KV, d0 = 4 * lane;
-    if (hh >= H + KV) {
-        const h4 y = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
-        *reinterpret_cast<h4*>(a.vc + ((int64_t)(a.off + t) * KV + (hh - H - KV)) * D + d0) = y;
-        return;
-    }
+// One head row held by a wave (lane l: dims 4l .. 4l+3): x * (1 / sqrt(sum x^2 / 256 + 1e-6)) * w (a wave-wide
+// sum), then on dims d < rot: x' = x cos - x[d + rot/2] sin (first half), x cos + x[d - rot/2] sin (second half),
+// with the partner element from lane l +- rot/8 (rot is a multiple of 8, so a lane's four dims sit on one side
+// of rot/2). All 64 lanes take part.
+__device__ __forceinline__ f4 norm_rope(f4 x, f4 w, f4 cs, f4 sn, int rot, int lane) {
+    const int d0 = 4 * lane;
     float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
     const float r = 1.0f / sqrtf(ss / 256.0f + 1e-6f);
 #pragma unroll
     for (int e = 0; e < 4; e++) x[e] = x[e] * r * w[e];
-    const int half = a.rot >> 1;
-    if (d0 < a.rot) {
-        // partner dims d -+ half are in lane l -+ half/4 (rot is a multiple of 8, so a lane's four dims sit on
-        // one side of `half`); the partner lanes are all inside this branch
+    const int half = rot >> 1;
+    if (d0 < rot) {
+        // the partner lanes are all inside this branch
         const int pl = d0 < half ? lane + (half >> 2) : lane - (half >> 2);
         f4 xp;
 #pragma unroll
@@ -79,6 +64,34 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, int t, int hh, f4 x,
 #pragma unroll
         for (int e = 0; e < 4; e++) x[e] = d0 < half ? x[e] * cs[e] - xp[e] * sn[e] : x[e] * cs[e] + xp[e] * sn[e];
     }
+    return x;
+}
+
+struct PrepArgs {
+    const float* qp;         // q rows: element t*qp_ts + h*qp_hs + d (the q half of the q_proj output)
+    int64_t qp_ts, qp_hs;
+    const float* kp;         // [T][KV][256]
+    const float* vp;         // [T][KV][256]
+    RopeParams rp;           // npos = T
+    float* q;                // element t*q_ts + h*q_hs + d: fp32 ...
+    uint16_t* q16;           // ... or fp16 bits when non-null; both null: the q rows are skipped
+    int64_t q_ts, q_hs;
+    uint16_t* kc;            // fp16 [cap][KV][256]: rows off .. off+T-1 written
+    uint16_t* vc;
+    int T, off, H, KV;
+};
+
+// One head row of token t: q heads [0, H), k heads [H, H+KV), v heads [H+KV, H+2KV); lane l holds dims
+// 4l .. 4l+3 (x, already loaded; w the norm weights of those dims, cs/sn the token's rotation). q and k: norm
+// and rotation (norm_rope); v: copied. k and v are rounded to fp16 (nearest even) into cache row off + t.
+__device__ __forceinline__ void prep_row(const PrepArgs& a, int t, int hh, f4 x, f4 w, f4 cs, f4 sn, int lane) {
+    const int H = a.H, KV = a.KV, d0 = 4 * lane;
+    if (hh >= H + KV) {
+        const h4 y = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+        *reinterpret_cast<h4*>(a.vc + ((int64_t)(a.off + t) * KV + (hh - H - KV)) * D + d0) = y;
+        return;
+    }
+    x = norm_rope(x, w, cs, sn, a.rp.rot, lane);
     if (hh < H) {
         if (a.q16) {
             const h4 y = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
@@ -94,18 +107,20 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, int t, int hh, f4 x,
 
 constexpr int PREP_B = 4;  // head rows per wave with their loads in flight together
 
-// Grid (T) x 4 waves: block = token t; wave w takes head rows w, w + 4, w + 8, ..., PREP_B of them at a time with
-// all their loads issued before the first is used (one row per wave left too few bytes in flight per CU to
-// reach the HBM rate). The norm weights and the token's sin/cos are fetched once per wave, before the rows.
+// Grid (T) x 4 waves: block = token t; wave w takes head rows h_first + w, + 4, + 8, ..., PREP_B of them at a
+// time with all their loads issued before the first is used (one row per wave left too few bytes in flight per
+// CU to reach the HBM rate). h_first = H when no q output is asked for (K/V rows only). The norm weights and the
+// token's sin/cos are fetched once per wave, before the rows.
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.H, KV = a.KV, nh = H + 2 * KV, d0 = 4 * lane;
+    const int h_first = (a.q || a.q16) ? 0 : H;
     const int64_t kvd = (int64_t)KV * D;
-    const f4 wq = *reinterpret_cast<const f4*>(a.qn + d0);
-    const f4 wk = *reinterpret_cast<const f4*>(a.kn + d0);
+    const f4 wq = *reinterpret_cast<const f4*>(a.rp.qn + d0);
+    const f4 wk = *reinterpret_cast<const f4*>(a.rp.kn + d0);
     f4 cs, sn;
-    prep_angles(a, t, d0, cs, sn);
-    for (int h0 = wave; h0 < nh; h0 += 4 * PREP_B) {
+    rope_angles(a.rp, t, d0, cs, sn);
+    for (int h0 = h_first + wave; h0 < nh; h0 += 4 * PREP_B) {
         f4 x[PREP_B];
 #pragma unroll
         for (int b = 0; b < PREP_B; b++) {

@@ -202,6 +202,17 @@ bn_status bn_attn_prep(bn_ctx* ctx, bn_stream stream, const bn_prep_args* a);
 /* gate_rotate (kernels/gate_rotate.comp:11-26): gate, signs, FWHT-512, 1/sqrt(512); `xr` is o_proj's input. */
 bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a);
 
+/* The attention arm of one layer in one call (model.rs:828-893: attn_prep, attn_split, attn_combine, gate_rotate):
+ * p's raw rows (q_proj's q half, k_proj, v_proj) are normed and rotated as bn_attn_prep does, the K/V rows land
+ * in the cache, and `a` attends, gates and (with a->signs) rotates. For T <= 16 (a decode step, verify rows)
+ * attn_prep runs inside the decode kernel's prologue: one row is one split launch (plus the split merge when the
+ * keys are split), several rows have their K/V rows written by the prep kernel first. For T > 16 (prefill) the
+ * prep kernel writes q to p->q (fp16 with BN_Q_F16, the cheaper form for the prefill kernel) and the K/V rows,
+ * then the prefill kernels run. p and a describe the same rows (T, off, H, KV, cap, kc, vc); a->q, a->k_new and
+ * a->v_new are NULL and a->flags is 0. p->q is needed only for T > 16; otherwise it may be NULL and is not
+ * written. Same workspace as bn_attn_forward. */
+bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, const bn_attn_args* a);
+
 #ifdef __cplusplus
 }
 #endif
