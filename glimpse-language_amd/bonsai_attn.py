@@ -25,7 +25,7 @@ EXPORTS = (
     "bn_attn_workspace_size", "bn_ragged_workspace_size", "bn_attn_check", "bn_ragged_check",
     "bn_workspace_clear", "bn_attn_forward", "bn_attn_decode", "bn_attn_verify", "bn_attn_prefill",
     "bn_attn_append", "bn_attn_decode_ragged", "bn_prep_check", "bn_rotate_check", "bn_attn_prep",
-    "bn_gate_rotate", "bn_attn_layer",
+    "bn_gate_rotate", "bn_attn_layer", "bn_layer_check",
 )
 
 
@@ -128,6 +128,8 @@ def load(path=LIB_PATH):
     lib.bn_gate_rotate.restype = ctypes.c_int
     lib.bn_attn_layer.argtypes = [P, P, ctypes.POINTER(PrepArgs), ctypes.POINTER(AttnArgs)]
     lib.bn_attn_layer.restype = ctypes.c_int
+    lib.bn_layer_check.argtypes = [ctypes.POINTER(PrepArgs), ctypes.POINTER(AttnArgs)]
+    lib.bn_layer_check.restype = ctypes.c_int
     _lib = lib
     return lib
 

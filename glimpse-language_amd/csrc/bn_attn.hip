@@ -662,6 +662,11 @@ bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_a
 
 bn_status bn_prep_check(const bn_prep_args* a) { return check_prep(a, g_check_err); }
 
+bn_status bn_layer_check(const bn_prep_args* p, const bn_attn_args* a) {
+    bn_attn_args m;
+    return check_layer(p, a, &m, g_check_err);
+}
+
 bn_status bn_rotate_check(const bn_rotate_args* a) { return check_rotate(a, g_check_err); }
 
 bn_status bn_attn_prep(bn_ctx* ctx, bn_stream stream, const bn_prep_args* a) {

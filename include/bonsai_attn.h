@@ -197,6 +197,7 @@ bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_a
 /* ---- either side of the attention call ------------------------------------------------------------ */
 bn_status bn_prep_check(const bn_prep_args* a);
 bn_status bn_rotate_check(const bn_rotate_args* a);
+bn_status bn_layer_check(const bn_prep_args* p, const bn_attn_args* a);
 /* attn_prep (kernels/attn_prep.comp:29-59): norms, mRoPE, fp16 K/V append. */
 bn_status bn_attn_prep(bn_ctx* ctx, bn_stream stream, const bn_prep_args* a);
 /* gate_rotate (kernels/gate_rotate.comp:11-26): gate, signs, FWHT-512, 1/sqrt(512); `xr` is o_proj's input. */

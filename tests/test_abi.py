@@ -190,3 +190,39 @@ def test_rotate_check(lib, mutate):
     assert ba.last_check_error()
     assert lib.bn_rotate_check(None) == ba.BN_EINVAL
     assert lib.bn_prep_check(None) == ba.BN_EINVAL
+
+
+def layer_pair(T=1, off=100, H=8, KV=2):
+    p = good_prep(T=T, off=off, H=H, KV=KV)
+    a = ba.AttnArgs()
+    a.T, a.off, a.H, a.KV, a.cap = T, off, H, KV, p.cap
+    a.kc, a.vc = p.kc, p.vc
+    a.out, a.o_ts, a.o_hs = 0x500000, H * 256, 256
+    a.gate, a.g_ts, a.g_hs = p.qp + 1024, H * 512, 512
+    probe = ba.AttnArgs()
+    ctypes.pointer(probe)[0] = a
+    probe.q, probe.q_ts, probe.q_hs, probe.k_new, probe.v_new = p.qp, p.qp_ts, p.qp_hs, p.kp, p.vp
+    need = ba.workspace_size(probe)
+    a.ws, a.ws_bytes = (0x600000 if need else None), need
+    return p, a
+
+
+def test_layer_check(lib):
+    p, a = layer_pair()
+    assert lib.bn_layer_check(p, a) == ba.BN_OK
+    p.q = None                                   # q scratch not needed up to 16 rows
+    assert lib.bn_layer_check(p, a) == ba.BN_OK
+    p2, a2 = layer_pair(T=40, off=0)
+    p2.q = None                                  # ... but needed for a prefill
+    assert lib.bn_layer_check(p2, a2) == ba.BN_EINVAL
+    p, a = layer_pair()
+    a.q = p.qp                                   # the attention args take no q, k_new, v_new
+    assert lib.bn_layer_check(p, a) == ba.BN_EINVAL
+    p, a = layer_pair()
+    a.off = 99                                   # both describe the same rows
+    assert lib.bn_layer_check(p, a) == ba.BN_EINVAL
+    p, a = layer_pair(T=1, off=5000)
+    a.ws_bytes = 0                               # a multi-split decode needs the workspace
+    assert lib.bn_layer_check(p, a) == ba.BN_ENOWS
+    assert lib.bn_layer_check(None, a) == ba.BN_EINVAL
+    assert lib.bn_attn_layer(None, None, None, None) == ba.BN_EINVAL
