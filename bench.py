@@ -225,6 +225,24 @@ class Workloads:
                     gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
 
+    def kv_copy(self, steps, warmup, n_layers, KV, length, cap, seed=0xB0A5A109):
+        """bn_kv_copy: the used rows of n_layers fp16 caches into a prefix-sized snapshot (encode_copy_state)."""
+        torch, ba, ctx = self.torch, self.ba, self.ctx
+        g = self._gen(seed)
+        kc = torch.randn(n_layers, cap, KV, D, device="cuda", generator=g).half().view(torch.int16)
+        vc = torch.randn(n_layers, cap, KV, D, device="cuda", generator=g).half().view(torch.int16)
+        sk = torch.empty(n_layers, length, KV, D, device="cuda", dtype=torch.int16)
+        sv = torch.empty_like(sk)
+        src, dst = ba.kv_state(kc, vc, length), ba.kv_state(sk, sv, 0)
+
+        def step():
+            ba.kv_copy(ctx, src, dst)
+
+        ms, wall = time_steps(torch, step, steps, warmup)
+        nbytes = 2 * 2 * n_layers * length * KV * D * 2  # K and V, read and written
+        return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
+
+
 def measured_traffic(name):
     """HBM bytes per step from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ (its
     `traffic_bytes_per_step:` line), or (None, None) when the summary is absent."""
@@ -277,7 +295,7 @@ def cpu_baseline(budget_s=10.0, H=16, KV=4, L=8192, nseq=2):
 
 ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix",
        "decode_8k_batch32_rotated", "prefill_4k_rotated", "verify_8_rotated", "prep_4k", "prep_decode",
-       "gate_rotate_4k", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k")
+       "gate_rotate_4k", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k", "kv_copy_8x4k")
 
 
 def main():
@@ -370,6 +388,10 @@ def main():
         log("layer_prefill_4k")
         res["layer_prefill_4k"] = r = W.layer(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0)
         log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
+    if "kv_copy_8x4k" in only:
+        log("kv_copy_8x4k")
+        res["kv_copy_8x4k"] = r = W.kv_copy(K, Wm, 8, 4, 4096, 8192)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")

@@ -25,8 +25,11 @@ EXPORTS = (
     "bn_attn_workspace_size", "bn_ragged_workspace_size", "bn_attn_check", "bn_ragged_check",
     "bn_workspace_clear", "bn_attn_forward", "bn_attn_decode", "bn_attn_verify", "bn_attn_prefill",
     "bn_attn_append", "bn_attn_decode_ragged", "bn_prep_check", "bn_rotate_check", "bn_attn_prep",
-    "bn_gate_rotate", "bn_attn_layer", "bn_layer_check",
+    "bn_gate_rotate", "bn_attn_layer", "bn_layer_check", "bn_kv_copy", "bn_kv_section_size", "bn_kv_section_save",
+    "bn_kv_section_check", "bn_kv_section_load",
 )
+KV_SECTION_MAGIC = b"BNKVF16\0"
+KV_SECTION_HEADER = 24
 
 
 class AttnArgs(ctypes.Structure):
@@ -80,6 +83,13 @@ class RotateArgs(ctypes.Structure):
     ]
 
 
+class KvState(ctypes.Structure):
+    _fields_ = [
+        ("kc", ctypes.c_void_p), ("vc", ctypes.c_void_p),
+        ("n_layers", ctypes.c_uint32), ("KV", ctypes.c_uint32), ("cap", ctypes.c_uint32), ("len", ctypes.c_uint32),
+    ]
+
+
 _lib = None
 
 
@@ -130,6 +140,17 @@ def load(path=LIB_PATH):
     lib.bn_attn_layer.restype = ctypes.c_int
     lib.bn_layer_check.argtypes = [ctypes.POINTER(PrepArgs), ctypes.POINTER(AttnArgs)]
     lib.bn_layer_check.restype = ctypes.c_int
+    K = ctypes.POINTER(KvState)
+    lib.bn_kv_copy.argtypes = [P, P, K, K]
+    lib.bn_kv_copy.restype = ctypes.c_int
+    lib.bn_kv_section_size.argtypes = [K]
+    lib.bn_kv_section_size.restype = ctypes.c_size_t
+    lib.bn_kv_section_save.argtypes = [P, P, K, P, ctypes.c_size_t]
+    lib.bn_kv_section_save.restype = ctypes.c_int
+    lib.bn_kv_section_check.argtypes = [P, ctypes.c_size_t, K, ctypes.POINTER(ctypes.c_uint32)]
+    lib.bn_kv_section_check.restype = ctypes.c_int
+    lib.bn_kv_section_load.argtypes = [P, P, P, ctypes.c_size_t, K, ctypes.POINTER(ctypes.c_uint32)]
+    lib.bn_kv_section_load.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -398,3 +419,44 @@ def attention_layer(ctx, ws, qp, kp, vp, q_norm, k_norm, pos, inv_freq, kc, vc, 
     st = ctx.lib.bn_attn_layer(ctx.h, ctx._stream(stream), ctypes.byref(p), ctypes.byref(a))
     ctx._check(st, "bn_attn_layer")
     return out
+
+
+def kv_state(kc, vc, length):
+    """bn_kv_state of caches kc/vc shaped [n_layers, cap, KV, 256] (fp16 or int16 views) with `length` rows used."""
+    st = KvState()
+    st.kc, st.vc = _ptr(kc), _ptr(vc)
+    st.n_layers, st.cap, st.KV = kc.shape[0], kc.shape[1], kc.shape[2]
+    st.len = length
+    return st
+
+
+def kv_copy(ctx, src, dst, stream=None):
+    """encode_copy_state's KV part: rows [0, src.len) of every layer from state src into state dst."""
+    st = ctx.lib.bn_kv_copy(ctx.h, ctx._stream(stream), ctypes.byref(src), ctypes.byref(dst))
+    ctx._check(st, "bn_kv_copy")
+
+
+def kv_section_save(ctx, state, stream=None):
+    """The KV section of a saved prefix (bytes)."""
+    n = load().bn_kv_section_size(ctypes.byref(state))
+    if n == 0:
+        raise BonsaiAttnError(BN_EINVAL, "bad KV state")
+    buf = ctypes.create_string_buffer(n)
+    st = ctx.lib.bn_kv_section_save(ctx.h, ctx._stream(stream), ctypes.byref(state), buf, n)
+    ctx._check(st, "bn_kv_section_save")
+    return buf.raw
+
+
+def kv_section_check(data, state):
+    """(status, len) of a KV section against a state, on the host."""
+    n = ctypes.c_uint32(0)
+    st = load().bn_kv_section_check(data, len(data), ctypes.byref(state), ctypes.byref(n))
+    return st, n.value
+
+
+def kv_section_load(ctx, data, state, stream=None):
+    """Loads a KV section into state's caches; returns its len."""
+    n = ctypes.c_uint32(0)
+    st = ctx.lib.bn_kv_section_load(ctx.h, ctx._stream(stream), data, len(data), ctypes.byref(state), ctypes.byref(n))
+    ctx._check(st, "bn_kv_section_load")
+    return n.value

@@ -500,6 +500,48 @@ bn_status check_layer(const bn_prep_args* p, const bn_attn_args* a, bn_attn_args
     return check_attn(m, 0, why);
 }
 
+bn_status check_kv_state(const bn_kv_state* s, char* why) {
+    if (!s) return set_err(why, BN_EINVAL, "state is NULL");
+    if (!s->kc || !s->vc || s->n_layers < 1 || s->KV < 1 || s->cap < 1)
+        return set_err(why, BN_EINVAL, "kc, vc, n_layers, KV and cap are required");
+    if (s->len > s->cap) return set_err(why, BN_EINVAL, "len %u exceeds cap %u", s->len, s->cap);
+    if ((uint64_t)s->n_layers * s->cap * s->KV * bn::D > (uint64_t)1 << 46)
+        return set_err(why, BN_EINVAL, "state too large");
+    return BN_OK;
+}
+
+size_t kv_rows_bytes(const bn_kv_state* s, uint32_t len) { return (size_t)len * s->KV * bn::D * sizeof(uint16_t); }
+
+void put_u32(uint8_t* p, uint32_t v) {
+    for (int i = 0; i < 4; i++) p[i] = (uint8_t)(v >> (8 * i));
+}
+uint32_t get_u32(const uint8_t* p) {
+    return (uint32_t)p[0] | (uint32_t)p[1] << 8 | (uint32_t)p[2] << 16 | (uint32_t)p[3] << 24;
+}
+
+bn_status check_kv_section(const void* src, size_t bytes, const bn_kv_state* s, uint32_t* len_out, char* why) {
+    bn_status st = check_kv_state(s, why);
+    if (st) return st;
+    if (!src || bytes < BN_KV_SECTION_HEADER) return set_err(why, BN_EINVAL, "section shorter than its header");
+    const uint8_t* h = static_cast<const uint8_t*>(src);
+    if (memcmp(h, BN_KV_SECTION_MAGIC, 8) != 0) return set_err(why, BN_EINVAL, "not a KV section (magic)");
+    if (get_u32(h + 8) != BN_KV_SECTION_VERSION) return set_err(why, BN_EINVAL, "KV section version %u", get_u32(h + 8));
+    if (get_u32(h + 12) != s->n_layers || get_u32(h + 16) != s->KV * (uint32_t)bn::D)
+        return set_err(why, BN_EINVAL, "KV section of %u layers x %u values per row, state has %u x %u", get_u32(h + 12),
+                       get_u32(h + 16), s->n_layers, s->KV * (uint32_t)bn::D);
+    const uint32_t len = get_u32(h + 20);
+    if (len > s->cap) return set_err(why, BN_EINVAL, "KV section of %u rows, cache holds %u", len, s->cap);
+    const size_t need = BN_KV_SECTION_HEADER + 2 * (size_t)s->n_layers * kv_rows_bytes(s, len);
+    if (bytes != need) return set_err(why, BN_EINVAL, "KV section of %zu bytes, %zu expected", bytes, need);
+    if (len_out) *len_out = len;
+    return BN_OK;
+}
+
+bn_status hip_err(bn_ctx* ctx, hipError_t e, const char* what) {
+    if (e == hipSuccess) return BN_OK;
+    return set_err(ctx->err, BN_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
 // kind: 0 forward, 1 decode, 2 verify, 3 prefill. One row is always a decode; verify-sized calls (T <= 16) of the
 // forward and verify entry points run as decodes of their rows; the rest take the MFMA prefill kernels.
 bn_status run(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int kind) {
@@ -658,6 +700,79 @@ bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_a
     d.KV = (int)a->KV;
     bind_workspace(d, p, a->ws);
     return launch_decode(ctx, (hipStream_t)stream, d, p);
+}
+
+bn_status bn_kv_copy(bn_ctx* ctx, bn_stream stream, const bn_kv_state* from, const bn_kv_state* to) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_kv_state(from, ctx->err);
+    if (!s) s = check_kv_state(to, ctx->err);
+    if (s) return s;
+    if (from->n_layers != to->n_layers || from->KV != to->KV)
+        return set_err(ctx->err, BN_EINVAL, "states of different shapes");
+    if (from->len > to->cap) return set_err(ctx->err, BN_EINVAL, "len %u exceeds the target's cap %u", from->len, to->cap);
+    if (from->len == 0) return BN_OK;
+    const size_t w = kv_rows_bytes(from, from->len);
+    const size_t sp = kv_rows_bytes(from, from->cap), dp = kv_rows_bytes(to, to->cap);
+    hipError_t e = hipMemcpy2DAsync(to->kc, dp, from->kc, sp, w, from->n_layers, hipMemcpyDeviceToDevice, (hipStream_t)stream);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(to->vc, dp, from->vc, sp, w, from->n_layers, hipMemcpyDeviceToDevice, (hipStream_t)stream);
+    return hip_err(ctx, e, "KV copy");
+}
+
+size_t bn_kv_section_size(const bn_kv_state* s) {
+    char why[256];
+    if (check_kv_state(s, why)) return 0;
+    return BN_KV_SECTION_HEADER + 2 * (size_t)s->n_layers * kv_rows_bytes(s, s->len);
+}
+
+bn_status bn_kv_section_save(bn_ctx* ctx, bn_stream stream, const bn_kv_state* s, void* dst, size_t dst_bytes) {
+    if (!ctx) return BN_EINVAL;
+    bn_status st = check_kv_state(s, ctx->err);
+    if (st) return st;
+    const size_t need = bn_kv_section_size(s);
+    if (!dst || dst_bytes < need) return set_err(ctx->err, BN_EINVAL, "section needs %zu bytes", need);
+    uint8_t* h = static_cast<uint8_t*>(dst);
+    memcpy(h, BN_KV_SECTION_MAGIC, 8);
+    put_u32(h + 8, BN_KV_SECTION_VERSION);
+    put_u32(h + 12, s->n_layers);
+    put_u32(h + 16, s->KV * (uint32_t)bn::D);
+    put_u32(h + 20, s->len);
+    const size_t rb = kv_rows_bytes(s, s->len), lp = kv_rows_bytes(s, s->cap);
+    hipError_t e = hipSuccess;
+    if (rb) {
+        uint8_t* body = h + BN_KV_SECTION_HEADER;
+        e = hipMemcpy2DAsync(body, rb, s->kc, lp, rb, s->n_layers, hipMemcpyDeviceToHost, (hipStream_t)stream);
+        if (e == hipSuccess)
+            e = hipMemcpy2DAsync(body + s->n_layers * rb, rb, s->vc, lp, rb, s->n_layers, hipMemcpyDeviceToHost,
+                                 (hipStream_t)stream);
+        if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    }
+    return hip_err(ctx, e, "KV section save");
+}
+
+bn_status bn_kv_section_check(const void* src, size_t src_bytes, const bn_kv_state* s, uint32_t* len_out) {
+    return check_kv_section(src, src_bytes, s, len_out, g_check_err);
+}
+
+bn_status bn_kv_section_load(bn_ctx* ctx, bn_stream stream, const void* src, size_t src_bytes, const bn_kv_state* s,
+                             uint32_t* len_out) {
+    if (!ctx) return BN_EINVAL;
+    uint32_t len = 0;
+    bn_status st = check_kv_section(src, src_bytes, s, &len, ctx->err);
+    if (st) return st;
+    const size_t rb = kv_rows_bytes(s, len), lp = kv_rows_bytes(s, s->cap);
+    hipError_t e = hipSuccess;
+    if (rb) {
+        const uint8_t* body = static_cast<const uint8_t*>(src) + BN_KV_SECTION_HEADER;
+        e = hipMemcpy2DAsync(s->kc, lp, body, rb, rb, s->n_layers, hipMemcpyHostToDevice, (hipStream_t)stream);
+        if (e == hipSuccess)
+            e = hipMemcpy2DAsync(s->vc, lp, body + s->n_layers * rb, rb, rb, s->n_layers, hipMemcpyHostToDevice,
+                                 (hipStream_t)stream);
+        if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+    }
+    st = hip_err(ctx, e, "KV section load");
+    if (!st && len_out) *len_out = len;
+    return st;
 }
 
 bn_status bn_prep_check(const bn_prep_args* a) { return check_prep(a, g_check_err); }

@@ -160,6 +160,24 @@ typedef struct bn_rotate_args {   /* pointers 16-byte aligned, strides multiples
     int64_t x_ts;
 } bn_rotate_args;
 
+/* The attention layers' part of a prefix-state snapshot (the reference's State: model.rs:174-186, 255-267; copied
+ * by encode_copy_state, model.rs:1072-1086; saved and loaded with state_parts, model.rs:1088-1099, by
+ * save_prefix / load_prefix, mod.rs:492-578): the used rows [0, len) of every attention layer's fp16 cache. */
+typedef struct bn_kv_state {
+    uint16_t* kc;                /* n_layers caches of cap rows each, [n_layers][cap][KV][256] fp16: layer i at */
+    uint16_t* vc;                /* kc + i * cap * KV * 256 (the reference's kc/vc buffers, in fp16) */
+    uint32_t n_layers, KV, cap;
+    uint32_t len;                /* rows in use, <= cap */
+} bn_kv_state;
+
+/* The KV section of a saved prefix file, little endian: the 8 bytes "BNKVF16\0", u32 version (1), u32 n_layers,
+ * u32 kv_width (KV * 256), u32 len, then rows [0, len) of every layer's K cache (fp16, layer after layer), then
+ * the same of V. The reference's file (magic BNSPFX01) holds the same rows in fp32 after its GDN and conv state;
+ * a runtime that keeps fp16 caches writes this section in their place and bumps its own magic. */
+#define BN_KV_SECTION_MAGIC "BNKVF16"
+#define BN_KV_SECTION_VERSION 1u
+#define BN_KV_SECTION_HEADER 24
+
 /* ---- context ---------------------------------------------------------------------------------- */
 bn_status bn_ctx_create(int device, bn_ctx** out);
 void bn_ctx_destroy(bn_ctx* ctx);
@@ -193,6 +211,23 @@ bn_status bn_attn_append(bn_ctx* ctx, bn_stream stream, const bn_attn_args* a);
 /* Ragged batched decode: no counterpart in the reference (one sequence per model there); each sequence
  * is the decode call above with its own cache rows. */
 bn_status bn_attn_decode_ragged(bn_ctx* ctx, bn_stream stream, const bn_ragged_args* a);
+
+/* ---- prefix-state snapshots -------------------------------------------------------------------------- */
+/* encode_copy_state's KV part: rows [0, from->len) of every layer from `from` into `to` (same n_layers and KV,
+ * to->cap >= from->len); one 2-D device copy on `stream`. to->len is the caller's to set. */
+bn_status bn_kv_copy(bn_ctx* ctx, bn_stream stream, const bn_kv_state* from, const bn_kv_state* to);
+/* Bytes of s's KV section (header + 2 * n_layers * len * KV * 256 * 2); 0 for a bad state. */
+size_t bn_kv_section_size(const bn_kv_state* s);
+/* Writes s's KV section (rows [0, s->len)) to host memory `dst` of dst_bytes >= bn_kv_section_size(s); waits for
+ * the copies, so `dst` is complete on return. */
+bn_status bn_kv_section_save(bn_ctx* ctx, bn_stream stream, const bn_kv_state* s, void* dst, size_t dst_bytes);
+/* Checks a KV section against s (magic, version, n_layers, KV, len <= s->cap, size) without device access and
+ * gives its len. */
+bn_status bn_kv_section_check(const void* src, size_t src_bytes, const bn_kv_state* s, uint32_t* len_out);
+/* Loads a checked section into rows [0, len) of s's caches (load_prefix's gpu::write of the KV parts); rows past
+ * len are untouched. Waits for the copies. A section that fails the check leaves the device untouched. */
+bn_status bn_kv_section_load(bn_ctx* ctx, bn_stream stream, const void* src, size_t src_bytes, const bn_kv_state* s,
+                             uint32_t* len_out);
 
 /* ---- either side of the attention call ------------------------------------------------------------ */
 bn_status bn_prep_check(const bn_prep_args* a);

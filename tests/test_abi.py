@@ -226,3 +226,38 @@ def test_layer_check(lib):
     assert lib.bn_layer_check(p, a) == ba.BN_ENOWS
     assert lib.bn_layer_check(None, a) == ba.BN_EINVAL
     assert lib.bn_attn_layer(None, None, None, None) == ba.BN_EINVAL
+
+
+def kv_state(n_layers=3, KV=2, cap=100, length=40):
+    s = ba.KvState()
+    s.kc, s.vc = 0x700000, 0x800000
+    s.n_layers, s.KV, s.cap, s.len = n_layers, KV, cap, length
+    return s
+
+
+def kv_section(n_layers, KV, length, body=None):
+    import struct
+    head = ba.KV_SECTION_MAGIC + struct.pack("<IIII", 1, n_layers, KV * 256, length)
+    n = 2 * n_layers * length * KV * 256 * 2
+    return head + (body if body is not None else bytes(n))
+
+
+def test_kv_section_format_checks(lib):
+    s = kv_state()
+    assert lib.bn_kv_section_size(s) == 24 + 2 * 3 * 40 * 2 * 256 * 2
+    good = kv_section(3, 2, 40)
+    assert len(good) == lib.bn_kv_section_size(s)
+    assert ba.kv_section_check(good, s) == (ba.BN_OK, 40)
+    assert ba.kv_section_check(kv_section(3, 2, 100), s) == (ba.BN_OK, 100)    # up to the cache's cap
+    assert ba.kv_section_check(kv_section(3, 2, 101), s)[0] == ba.BN_EINVAL    # more rows than the cache holds
+    assert ba.kv_section_check(kv_section(2, 2, 40), s)[0] == ba.BN_EINVAL     # other layer count
+    assert ba.kv_section_check(kv_section(3, 4, 40), s)[0] == ba.BN_EINVAL     # other row width
+    assert ba.kv_section_check(good[:-2], s)[0] == ba.BN_EINVAL                # truncated
+    assert ba.kv_section_check(good + b"\0", s)[0] == ba.BN_EINVAL             # trailing bytes
+    assert ba.kv_section_check(b"BNSPFX01" + good[8:], s)[0] == ba.BN_EINVAL   # the reference's fp32 file magic
+    bad_version = good[:8] + (2).to_bytes(4, "little") + good[12:]
+    assert ba.kv_section_check(bad_version, s)[0] == ba.BN_EINVAL
+    assert ba.kv_section_check(good[:10], s)[0] == ba.BN_EINVAL
+    s.len = 101
+    assert lib.bn_kv_section_size(s) == 0                                      # len beyond cap
+    assert lib.bn_kv_copy(None, None, None, None) == ba.BN_EINVAL
