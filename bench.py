@@ -243,6 +243,35 @@ class Workloads:
         return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, wall=wall)
 
 
+    def ternary(self, steps, warmup, T, K, os, add=False, seed=0xB0A5A10A):
+        """bn_ternary_matmul: y_i (+)= x W_i^T for the matrices sharing x (random 2-bit codes, fp16 scales)."""
+        torch, ba, ctx = self.torch, self.ba, self.ctx
+        g = self._gen(seed)
+        x = torch.randn(T, K, device="cuda", generator=g)
+        mats = []
+        for o in os:
+            w = torch.randint(-2 ** 31, 2 ** 31 - 1, (o, K // 16), device="cuda", dtype=torch.int32, generator=g)
+            sc = (0.02 * torch.rand(o, K // 128, device="cuda", generator=g) + 0.005).half().view(torch.int16)
+            mats.append((w, sc, torch.zeros(T, o, device="cuda")))
+
+        # the argument struct is built once: a step is the library call alone (its launch is a few microseconds,
+        # below what building the ctypes struct in Python costs)
+        import ctypes
+        args = ba.ternary_args(x, mats, add)
+        stream = ctx._stream(None)
+
+        def step():
+            ctx._check(ctx.lib.bn_ternary_matmul(ctx.h, stream, ctypes.byref(args)), "bn_ternary_matmul")
+
+        ms, wall = time_steps(torch, step, steps, warmup)
+        O = sum(os)
+        # codes and scales read once, x read, y written (and read with add)
+        nbytes = O * K // 4 + O * (K // 128) * 2 + T * K * 4 + T * O * 4 * (2 if add else 1)
+        flops = 2 * T * K * O
+        return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, flops=flops,
+                    tflops=flops / (ms * 1e-3) / 1e12, wall=wall)
+
+
 def measured_traffic(name):
     """HBM bytes per step from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ (its
     `traffic_bytes_per_step:` line), or (None, None) when the summary is absent."""
@@ -295,7 +324,18 @@ def cpu_baseline(budget_s=10.0, H=16, KV=4, L=8192, nseq=2):
 
 ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix",
        "decode_8k_batch32_rotated", "prefill_4k_rotated", "verify_8_rotated", "prep_4k", "prep_decode",
-       "gate_rotate_4k", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k", "kv_copy_8x4k")
+       "gate_rotate_4k", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k", "kv_copy_8x4k",
+       "qkv_decode_4b", "qkv_verify_8_4b", "qkv_prefill_4k_4b", "o_proj_decode_4b", "o_proj_prefill_4k_4b")
+# ternary projections of the 4B layer (hidden 2560, 16 q heads, 4 kv heads): q_proj 8192 rows (q and gate halves),
+# k_proj and v_proj 1024 rows each, all over the 2560-wide normed input; o_proj 2560 rows over the 4096-wide
+# rotated attention output, added into the residual
+TERNARY = {
+    "qkv_decode_4b": dict(T=1, K=2560, os=(8192, 1024, 1024)),
+    "qkv_verify_8_4b": dict(T=8, K=2560, os=(8192, 1024, 1024)),
+    "qkv_prefill_4k_4b": dict(T=4096, K=2560, os=(8192, 1024, 1024)),
+    "o_proj_decode_4b": dict(T=1, K=4096, os=(2560,), add=True),
+    "o_proj_prefill_4k_4b": dict(T=4096, K=4096, os=(2560,), add=True),
+}
 
 
 def main():
@@ -392,6 +432,12 @@ def main():
         log("kv_copy_8x4k")
         res["kv_copy_8x4k"] = r = W.kv_copy(K, Wm, 8, 4, 4096, 8192)
         log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    for name, cfg in TERNARY.items():
+        if name in only:
+            log(name)
+            big = cfg["T"] > 16
+            res[name] = r = W.ternary(max(2, K // 4) if big else K, max(1, Wm // 2) if big else Wm, **cfg)
+            log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s, {r['tflops']:.1f} TFLOP/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")

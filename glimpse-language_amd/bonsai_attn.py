@@ -26,7 +26,7 @@ EXPORTS = (
     "bn_workspace_clear", "bn_attn_forward", "bn_attn_decode", "bn_attn_verify", "bn_attn_prefill",
     "bn_attn_append", "bn_attn_decode_ragged", "bn_prep_check", "bn_rotate_check", "bn_attn_prep",
     "bn_gate_rotate", "bn_attn_layer", "bn_layer_check", "bn_kv_copy", "bn_kv_section_size", "bn_kv_section_save",
-    "bn_kv_section_check", "bn_kv_section_load",
+    "bn_kv_section_check", "bn_kv_section_load", "bn_ternary_check", "bn_ternary_matmul",
 )
 KV_SECTION_MAGIC = b"BNKVF16\0"
 KV_SECTION_HEADER = 24
@@ -93,6 +93,21 @@ class KvState(ctypes.Structure):
 _lib = None
 
 
+class TernaryMat(ctypes.Structure):
+    _fields_ = [
+        ("w", ctypes.c_void_p), ("s", ctypes.c_void_p), ("y", ctypes.c_void_p), ("lora_b", ctypes.c_void_p),
+        ("o", ctypes.c_uint32), ("y_ts", ctypes.c_int64),
+    ]
+
+
+class TernaryArgs(ctypes.Structure):
+    _fields_ = [
+        ("T", ctypes.c_uint32), ("k", ctypes.c_uint32), ("x", ctypes.c_void_p), ("x_ts", ctypes.c_int64),
+        ("n_mats", ctypes.c_uint32), ("add", ctypes.c_uint32), ("mat", TernaryMat * 3),
+        ("lora_u", ctypes.c_void_p), ("lora_us", ctypes.c_int64), ("lora_r", ctypes.c_uint32),
+    ]
+
+
 def load(path=LIB_PATH):
     """Loads the HIP library (raises if it has not been built)."""
     global _lib
@@ -151,6 +166,10 @@ def load(path=LIB_PATH):
     lib.bn_kv_section_check.restype = ctypes.c_int
     lib.bn_kv_section_load.argtypes = [P, P, P, ctypes.c_size_t, K, ctypes.POINTER(ctypes.c_uint32)]
     lib.bn_kv_section_load.restype = ctypes.c_int
+    lib.bn_ternary_check.argtypes = [ctypes.POINTER(TernaryArgs)]
+    lib.bn_ternary_check.restype = ctypes.c_int
+    lib.bn_ternary_matmul.argtypes = [P, P, ctypes.POINTER(TernaryArgs)]
+    lib.bn_ternary_matmul.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -460,3 +479,28 @@ def kv_section_load(ctx, data, state, stream=None):
     st = ctx.lib.bn_kv_section_load(ctx.h, ctx._stream(stream), data, len(data), ctypes.byref(state), ctypes.byref(n))
     ctx._check(st, "bn_kv_section_load")
     return n.value
+
+
+def ternary_args(x, mats, add=False, lora_u=None, lora_r=0):
+    """bn_ternary_args: x [T, K] float32 (unit stride inside a row); mats: up to three (w, s, y) or
+    (w, s, y, lora_b) with w int32/uint32 [O, K/16], s fp16/int16 [O, K/128], y [T, O] float32."""
+    a = TernaryArgs()
+    a.T, a.k = x.shape[0], x.shape[1]
+    a.x, a.x_ts = _ptr(x), x.stride(0)
+    a.n_mats = len(mats)
+    a.add = int(bool(add))
+    for i, m in enumerate(mats):
+        w, sc, y = m[0], m[1], m[2]
+        lb = m[3] if len(m) > 3 else None
+        a.mat[i].w, a.mat[i].s, a.mat[i].y, a.mat[i].lora_b = _ptr(w), _ptr(sc), _ptr(y), _ptr(lb)
+        a.mat[i].o = w.shape[0]
+        a.mat[i].y_ts = y.stride(0)
+    a.lora_u = _ptr(lora_u)
+    a.lora_us = lora_u.stride(0) if lora_u is not None else 0
+    a.lora_r = lora_r
+    return a
+
+
+def ternary_matmul(ctx, x, mats, add=False, lora_u=None, lora_r=0, stream=None):
+    """bn_ternary_matmul: y_i (+)= x W_i^T (+ LoRA) for each (w, s, y[, lora_b]) in mats; y tensors are written."""
+    ctx.call("bn_ternary_matmul", ternary_args(x, mats, add, lora_u, lora_r), stream)

@@ -13,6 +13,7 @@
 #include "bn_flash.h"
 #include "bn_prefill.h"
 #include "bn_prep.h"
+#include "bn_ternary.h"
 #include "bn_util_kernels.h"
 
 struct bn_ctx {
@@ -542,6 +543,91 @@ bn_status hip_err(bn_ctx* ctx, hipError_t e, const char* what) {
     return set_err(ctx->err, BN_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
 }
 
+bn_status check_ternary(const bn_ternary_args* a, char* why) {
+    if (!a) return set_err(why, BN_EINVAL, "args is NULL");
+    if (a->T < 1 || a->T > (1u << 24)) return set_err(why, BN_EINVAL, "T must be in 1..2^24 (T=%u)", a->T);
+    if (a->k < 128 || (a->k & 127) || a->k > (1u << 20))
+        return set_err(why, BN_EINVAL, "k must be a multiple of 128 in 128..2^20 (k=%u)", a->k);
+    if (a->n_mats < 1 || a->n_mats > 3) return set_err(why, BN_EINVAL, "n_mats must be 1..3 (n_mats=%u)", a->n_mats);
+    if (!a->x || !aligned16(a->x)) return set_err(why, BN_EINVAL, "x is required and must be 16-byte aligned");
+    if (a->T > 1 && (a->x_ts < (int64_t)a->k || (a->x_ts & 3)))
+        return set_err(why, BN_EINVAL, "x_ts must be a multiple of 4 and at least k");
+    if (a->add > 1) return set_err(why, BN_EINVAL, "add must be 0 or 1");
+    if (a->lora_r > 4096) return set_err(why, BN_EINVAL, "lora_r must be at most 4096");
+    if (a->lora_r && (!a->lora_u || a->lora_us < 0 || (a->T > 1 && a->lora_us < (int64_t)a->n_mats * a->lora_r)))
+        return set_err(why, BN_EINVAL, "lora_u is required with lora_r, lora_us at least n_mats * lora_r");
+    int64_t rows = 0;
+    for (uint32_t i = 0; i < a->n_mats; ++i) {
+        const bn_ternary_mat& m = a->mat[i];
+        if (!m.w || !m.s || !m.y) return set_err(why, BN_EINVAL, "mat[%u]: w, s and y are required", i);
+        if (!aligned16(m.w) || ((uintptr_t)m.s & 1) || ((uintptr_t)m.y & 3) || ((uintptr_t)m.lora_b & 1))
+            return set_err(why, BN_EINVAL, "mat[%u]: w must be 16-byte aligned, s, y and lora_b element aligned", i);
+        if (m.o < 64 || (m.o & 63) || m.o > (1u << 24))
+            return set_err(why, BN_EINVAL, "mat[%u]: o must be a multiple of 64 in 64..2^24 (o=%u)", i, m.o);
+        if (a->T > 1 && m.y_ts < (int64_t)m.o) return set_err(why, BN_EINVAL, "mat[%u]: y_ts must be at least o", i);
+        if (m.lora_b && !a->lora_r) return set_err(why, BN_EINVAL, "mat[%u]: lora_b given with lora_r = 0", i);
+        rows += m.o;
+    }
+    if (rows > (1 << 30)) return set_err(why, BN_EINVAL, "too many rows");
+    return BN_OK;
+}
+
+// K split of the small-T MFMA kernel: 4 ways when each quarter of K is whole 64-column chunks, else 2 (k is a
+// multiple of 128)
+int tern_ksplit(uint32_t k) { return (k % (4 * bn::TERN_KC) == 0) ? 4 : 2; }
+
+bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
+    bn::TernArgs t{};
+    int64_t rows = 0;
+    for (uint32_t i = 0; i < 3; ++i) {
+        const bn_ternary_mat& m = a->mat[i < a->n_mats ? i : 0];
+        t.m[i].w = m.w;
+        t.m[i].s = m.s;
+        t.m[i].y = m.y;
+        t.m[i].lb = m.lora_b;
+        t.m[i].o = i < a->n_mats ? (int)m.o : 0;
+        t.m[i].y_ts = m.y_ts;
+        if (i < a->n_mats) rows += m.o;
+    }
+    t.n_mats = (int)a->n_mats;
+    t.rows = (int)rows;
+    t.x = a->x;
+    t.x_ts = a->x_ts;
+    t.T = (int)a->T;
+    t.K = (int)a->k;
+    t.add = (int)a->add;
+    t.lu = a->lora_u;
+    t.lu_ts = a->lora_us;
+    t.lr = (int)a->lora_r;
+    if (a->T <= 4) {
+        const dim3 grid((unsigned)ceil_div(rows, 4 * bn::TERN_ROWS_WAVE));
+        switch (a->T) {
+            case 1: hipLaunchKernelGGL(bn::tern_rows_kernel<1>, grid, dim3(256), 0, st, t); break;
+            case 2: hipLaunchKernelGGL(bn::tern_rows_kernel<2>, grid, dim3(256), 0, st, t); break;
+            case 3: hipLaunchKernelGGL(bn::tern_rows_kernel<3>, grid, dim3(256), 0, st, t); break;
+            default: hipLaunchKernelGGL(bn::tern_rows_kernel<4>, grid, dim3(256), 0, st, t); break;
+        }
+        return launched(ctx, "tern_rows_kernel");
+    }
+    if (a->T <= 32) {
+        // one 32-token tile, 64 rows per block, K split over the block's waves
+        const int row_tiles = (int)(rows / 64);
+        const dim3 grid((unsigned)row_tiles);
+        if (tern_ksplit(a->k) == 4)
+            hipLaunchKernelGGL((bn::tern_mfma_kernel<1, 4, 1>), grid, dim3(256), 0, st, t, row_tiles);
+        else
+            hipLaunchKernelGGL((bn::tern_mfma_kernel<1, 2, 1>), grid, dim3(128), 0, st, t, row_tiles);
+        return launched(ctx, "tern_mfma_kernel<1>");
+    }
+    constexpr int MT = BN_TERN_PF_MT;
+    const int row_tiles = (int)ceil_div(rows, 256);
+    const int64_t blocks = (int64_t)row_tiles * ceil_div(a->T, 32 * MT);
+    if (blocks > INT32_MAX) return set_err(ctx->err, BN_EINVAL, "T * rows too large for one launch");
+    hipLaunchKernelGGL((bn::tern_mfma_kernel<MT, 1, 4, BN_TERN_PF_OCC>), dim3((unsigned)blocks), dim3(256), 0, st, t,
+                       row_tiles);
+    return launched(ctx, "tern_mfma_kernel (prefill)");
+}
+
 // kind: 0 forward, 1 decode, 2 verify, 3 prefill. One row is always a decode; verify-sized calls (T <= 16) of the
 // forward and verify entry points run as decodes of their rows; the rest take the MFMA prefill kernels.
 bn_status run(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int kind) {
@@ -829,6 +915,15 @@ bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, co
     m.q_hs = p->q_hs;
     m.flags = p->flags;
     return run_flash(ctx, st, &m);
+}
+
+bn_status bn_ternary_check(const bn_ternary_args* a) { return check_ternary(a, g_check_err); }
+
+bn_status bn_ternary_matmul(bn_ctx* ctx, bn_stream stream, const bn_ternary_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_ternary(a, ctx->err);
+    if (s) return s;
+    return run_ternary(ctx, (hipStream_t)stream, a);
 }
 
 bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a) {

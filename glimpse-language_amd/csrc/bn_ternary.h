@@ -1,0 +1,396 @@
+// Ternary packed linears: Y[T, O] (+)= X[T, K] W[O, K]^T for up to three matrices sharing X, with the LoRA up
+// projection in the store (model.rs:455-639 qmm_lora / qmm / qmm_multi; kernels/qmv.glsl, qmv3.comp, qmv4.comp,
+// qmvr.comp, qmvx.comp, qmm3.comp; kernels.metal:248-500, 664-709).
+//
+// Weight format (kernels/qmv.glsl:1-2): row n of W is K/16 uint32 words, word j holding codes of k = 16j + e at
+// bits [2e, 2e+2); one fp16 scale per 128 codes, s[n * K/128 + k/128]; weight = scale * (code - 1).
+//
+// Two kernels:
+//   tern_rows_kernel<NT> (T <= 4): VALU. Lanes take words of 8 rows at a time; per word and token the reference's
+//     decode arithmetic, acc += s * (sum_e x_e * code_e - sum_e x_e) (qmv.glsl:22-35), then a wave sum.
+//   tern_mfma_kernel<MT, KS> (T > 4): v_mfma_f32_32x32x16_f16 with X as A (tokens) and W as B (rows). Weights are
+//     exact in fp16 ((code - 1) * scale is -s, 0, s or 2s); X is split into hi = fp16(x) and lo = fp16(x - hi), two
+//     MFMAs per tile, so each product carries 22 of x's 24 mantissa bits and every sum is fp32: the same result
+//     class as the reference's fp32 matmuls (qmm3.comp, the Metal qmm's float MMA), not an fp16 GEMM.
+//     Codes become fp16 through v_perm_b32 on a 4-byte table (no int->float conversion per code).
+// Both write y = (add ? y + v : v) + sum_j u[j] * B[n, j] (store_post, qmv.glsl:10-15).
+#pragma once
+#include "bn_device.h"
+
+namespace bn {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+struct TernMat {
+    const uint32_t* w;   // [o][K/16]
+    const uint16_t* s;   // [o][K/128] fp16
+    float* y;            // output row t at y + t * y_ts
+    const uint16_t* lb;  // LoRA B [o][lr] fp16, or null (no adapter on this member)
+    int o;
+    int64_t y_ts;
+};
+
+struct TernArgs {
+    TernMat m[3];
+    int n_mats;
+    int rows;            // sum of the members' o; rows of member i follow member i - 1
+    const float* x;      // token t at x + t * x_ts
+    int64_t x_ts;
+    int T, K;
+    int add;
+    const float* lu;     // LoRA u: token t, member i at lu + t * lu_ts + i * lr
+    int64_t lu_ts;
+    int lr;
+};
+
+// member of global row r; r becomes the member's row
+__device__ __forceinline__ int tern_member(const TernArgs& a, int& r) {
+    if (r < a.m[0].o) return 0;
+    r -= a.m[0].o;
+    if (r < a.m[1].o) return 1;
+    r -= a.m[1].o;
+    return 2;
+}
+// member i by value, through selects (a dynamic index into the kernel argument would copy it to scratch)
+__device__ __forceinline__ TernMat tern_mat(const TernArgs& a, int i) {
+    return i == 0 ? a.m[0] : (i == 1 ? a.m[1] : a.m[2]);
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// y = (add ? y + v : v) + LoRA (qmv.glsl:10-15 store_post, lora_acc summed in j order)
+__device__ __forceinline__ void tern_store(const TernArgs& a, const TernMat& m, int mi, int t, int n, float v) {
+    float* y = m.y + (int64_t)t * m.y_ts + n;
+    float yv = a.add ? *y + v : v;
+    if (a.lr > 0 && m.lb) {
+        const float* u = a.lu + (int64_t)t * a.lu_ts + (int64_t)mi * a.lr;
+        const uint16_t* b = m.lb + (int64_t)n * a.lr;
+        float acc = 0.0f;
+        for (int j = 0; j < a.lr; ++j) acc = fmaf(u[j], h2f(b[j]), acc);
+        yv = yv + acc;
+    }
+    *y = yv;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+constexpr int TERN_ROWS_WAVE = 4;  // rows per wave of tern_rows_kernel (block: 4 waves, 16 rows)
+
+// Sums of 4 values over the wave: lane l ends with the total of value (l >> 4) & 3 (7 exchanges instead of 24:
+// each step hands the partner the half of the values it does not keep).
+__device__ __forceinline__ float wave_sum4(const float (&v)[4], int lane) {
+    const bool up = lane & 32;
+    const float a = __shfl_xor(up ? v[0] : v[2], 32), b = __shfl_xor(up ? v[1] : v[3], 32);
+    const float k0 = (up ? v[2] : v[0]) + a, k1 = (up ? v[3] : v[1]) + b;
+    const bool b4 = lane & 16;
+    float x = (b4 ? k1 : k0) + __shfl_xor(b4 ? k0 : k1, 16);
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+// T = NT <= 4 tokens. Each wave: 4 rows of one member; lane l takes words j = l, l + 64, ..., the next word's
+// codes, scales and x loaded while the current one is summed.
+template <int NT>
+__global__ __launch_bounds__(256) void tern_rows_kernel(TernArgs a) {
+    constexpr int R = TERN_ROWS_WAVE;
+    const int lane = threadIdx.x & 63;
+    const int r0g = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (r0g >= a.rows) return;  // no barriers below
+    int r0 = r0g;
+    const int mi = tern_member(a, r0);
+    const TernMat m = tern_mat(a, mi);
+    const int K = a.K, kw = K >> 4, kg = K >> 7;
+    const uint32_t* wp = m.w + (int64_t)r0 * kw;
+    const uint16_t* sp = m.s + (int64_t)r0 * kg;
+    float acc[R][NT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[r][t] = 0.0f;
+    uint32_t wn[R];
+    uint16_t sn[R];
+    f4 xn[NT][4];
+    auto load = [&](int j) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wn[r] = wp[(int64_t)r * kw + j];
+            sn[r] = sp[(int64_t)r * kg + (j >> 3)];
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xn[t][q] = reinterpret_cast<const f4*>(a.x + (int64_t)t * a.x_ts + 16 * j)[q];
+    };
+    if (lane < kw) load(lane);
+    for (int j = lane; j < kw; j += 64) {
+        uint32_t wc[R];
+        float sc[R], xv[NT][16], xs[NT];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wc[r] = wn[r];
+            sc[r] = h2f(sn[r]);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float s = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    xv[t][4 * q + e] = xn[t][q][e];
+                    s += xn[t][q][e];
+                }
+            xs[t] = s;
+        }
+        if (j + 64 < kw) load(j + 64);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            // code e = 4b + s sits in byte b of (wd >> 2s) & 0x03030303 (one v_cvt_f32_ubyte per code)
+            float c[16];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t q = (wc[r] >> (2 * s)) & 0x03030303u;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) c[4 * b + s] = (float)((q >> (8 * b)) & 0xFFu);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) d = fmaf(xv[t][e], c[e], d);
+                acc[r][t] = fmaf(sc[r], d - xs[t], acc[r][t]);
+            }
+        }
+    }
+    // lanes 16 r (+ t) hold row r's sums; lanes 16 r + t store token t
+    float mine = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float v[4] = {acc[0][t], acc[1][t], acc[2][t], acc[3][t]};
+        const float sum = wave_sum4(v, lane);
+        if ((lane & 15) == t) mine = sum;
+    }
+    if ((lane & 15) < NT) tern_store(a, m, mi, lane & 15, r0 + (lane >> 4), mine);
+}
+
+// ---- MFMA kernel --------------------------------------------------------------------------------------------
+constexpr int TERN_KC = 64;  // k per staged chunk (4 MFMA k-steps of 16)
+// prefill kernel shape: 32-token tiles per wave and waves per SIMD it is compiled for
+#ifndef BN_TERN_PF_MT
+#define BN_TERN_PF_MT 2
+#endif
+#ifndef BN_TERN_PF_OCC
+#define BN_TERN_PF_OCC 2
+#endif
+
+// 8 codes of word `wd` as fp16 (code - 1) * s: slots 2i, 2i+1 = codes 4kg + i, 12... see the A layout below.
+// wd2 = kg ? wd : wd << 8 puts the lane's codes (4kg + i, 8 + 4kg + i) at bits [8 + 2i, ..) and [24 + 2i, ..).
+__device__ __forceinline__ h8 tern_decode8(uint32_t wd2, h2 s2) {
+    h8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // selector bytes 1 and 3 = the two codes (0..3, table bytes), bytes 0 and 2 = 0x0C (zero byte)
+        const uint32_t sel = ((wd2 >> (2 * i)) & 0x03000300u) | 0x000C000Cu;
+        // table: byte c = high byte of fp16(c - 1): -1 0xBC00, 0 0x0000, 1 0x3C00, 2 0x4000
+        const uint32_t hv = __builtin_amdgcn_perm(0u, 0x403C00BCu, sel);
+        const h2 v = __builtin_bit_cast(h2, hv) * s2;  // exact: (code - 1) * s is -s, 0, s or 2s
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+// A block whose waves each stage their own K range (KS > 1, one row group) orders its LDS writes and reads within
+// the wave (LDS instructions of one wave complete in order); a block whose waves share the staged tile syncs.
+template <int KS>
+__device__ __forceinline__ void tern_sync() {
+    if constexpr (KS > 1) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+        __syncthreads();
+    }
+}
+
+// MT 32-token tiles x 2 32-row tiles per wave; KS waves split K (their partial sums meet in LDS in ks order), RG
+// waves split rows (KS > 1 only with RG = 1). Block: 64 * KS * RG threads, 32 * MT tokens x 64 * RG rows.
+//
+// A layout in LDS, per k-split group: hi[4 q][2 kg][32 MT m][8 slots] fp16, then lo the same. Slot i of (q, kg, m)
+// holds x[m][k0 + 16q + 4kg + 8(i & 1) + (i >> 1)], the k order tern_decode8 gives the B operand, so each lane's A
+// operand (m = lane % 32, kg = lane / 32) is one 16-byte LDS read.
+template <int MT, int KS, int RG, int OCC = 1>
+__global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row_tiles) {
+    static_assert(KS * RG <= 4 && (KS == 1 || (RG == 1 && MT == 1)), "split-K blocks are one token tile, one row group");
+    constexpr int BM = 32 * MT;        // tokens per block
+    constexpr int GROUP_H = 2 * 8 * BM * 8;  // fp16 per k-split group (hi and lo): 4 q * 2 kg * BM * 8 * 2
+    // one buffer, two syncs per chunk: a second buffer costs registers and occupancy (3 -> 2 waves per SIMD for
+    // the prefill shape) and measured slower on MI355X
+    __shared__ __attribute__((aligned(16))) _Float16 lds[KS * GROUP_H];
+    static_assert(KS * GROUP_H * 2 <= 65536, "LDS");
+    static_assert(KS * 32 * MT * 64 * 4 <= KS * GROUP_H * 2 || KS == 1, "reduction buffer fits the A buffer");
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rg = wave / KS, ks = wave % KS;
+    const int tile = blockIdx.x;
+    const int rt = tile % row_tiles, tt = tile / row_tiles;
+    const int t0 = tt * BM;
+    const int rbase_g = (rt * RG + rg) * 64;  // first global row of this wave
+    const bool active = rbase_g < a.rows;
+    int rbase = active ? rbase_g : 0;
+    const int mi = tern_member(a, rbase);
+    const TernMat m = tern_mat(a, mi);
+
+    const int K = a.K, kw = K >> 4, kg = K >> 7;
+    const int klen = K / KS, kbase = ks * klen, nchunk = klen / TERN_KC;
+
+    // staging: group thread gt of 64 * RG takes units u = gt + i * 64 * RG, u = (m * 4 + q) * 2 + kgu
+    constexpr int GT = 64 * RG, UPT = 8 * BM / GT;
+    const int gt = rg * 64 + lane;
+    _Float16* glds = lds + ks * GROUP_H;
+    f4 xa[UPT], xb[UPT];
+    auto load_x = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+            const int u = gt + i * GT;
+            const int mm = u >> 3, q = (u >> 1) & 3, kgu = u & 1;
+            // token rows past T are neither loaded nor staged: their A rows only feed outputs that are not stored
+            if (t0 + mm < a.T) {
+                const float* p = a.x + (int64_t)(t0 + mm) * a.x_ts + kbase + c * TERN_KC + 16 * q + 4 * kgu;
+                xa[i] = *reinterpret_cast<const f4*>(p);
+                xb[i] = *reinterpret_cast<const f4*>(p + 8);
+            }
+        }
+    };
+    auto store_x = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+            const int u = gt + i * GT;
+            const int mm = u >> 3, q = (u >> 1) & 3, kgu = u & 1;
+            if (t0 + mm >= a.T) continue;
+            h8 hi, lo;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                hi[2 * s] = (_Float16)xa[i][s];
+                hi[2 * s + 1] = (_Float16)xb[i][s];
+                lo[2 * s] = (_Float16)(xa[i][s] - (float)hi[2 * s]);
+                lo[2 * s + 1] = (_Float16)(xb[i][s] - (float)hi[2 * s + 1]);
+            }
+            const int off = ((q * 2 + kgu) * BM + mm) * 8;
+            *reinterpret_cast<h8*>(glds + off) = hi;
+            *reinterpret_cast<h8*>(glds + 8 * BM * 8 + off) = lo;
+        }
+    };
+
+    // B: lane (n = lane % 32, kgl = lane / 32) of row tile nt reads row rbase + 32 nt + n
+    const int n = lane & 31, kgl = lane >> 5;
+    const uint32_t* wrow[2];
+    const uint16_t* srow[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int64_t row = rbase + 32 * nt + n;
+        wrow[nt] = m.w + row * kw + kbase / 16;
+        srow[nt] = m.s + row * kg;
+    }
+    u4 wv[2];
+    auto load_w = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) wv[nt] = *reinterpret_cast<const u4*>(wrow[nt] + c * (TERN_KC / 16));
+    };
+
+    f16x acc[MT][2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][nt][e] = 0.0f;
+
+    const int shift = kgl ? 0 : 8;
+    auto scales = [&](int c, h2 (&s2)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            const _Float16 sv = active ? __builtin_bit_cast(_Float16, srow[nt][(kbase + c * TERN_KC) >> 7]) : (_Float16)0;
+            s2[nt] = h2{sv, sv};
+        }
+    };
+    load_x(0);
+    if (active) load_w(0);
+    for (int c = 0; c < nchunk; ++c) {
+        tern_sync<KS>();  // the previous chunk's A reads are done
+        store_x();
+        u4 wcur[2] = {wv[0], wv[1]};
+        h2 s2[2];
+        scales(c, s2);
+        tern_sync<KS>();
+        if (c + 1 < nchunk) {
+            load_x(c + 1);
+            if (active) load_w(c + 1);
+        }
+        if (active) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                h8 b[2];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) b[nt] = tern_decode8(wcur[nt][q] << shift, s2[nt]);
+                h8 ah[MT], al[MT];
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+                    const int off = ((q * 2 + kgl) * BM + 32 * i + n) * 8;
+                    ah[i] = *reinterpret_cast<const h8*>(glds + off);
+                    al[i] = *reinterpret_cast<const h8*>(glds + 8 * BM * 8 + off);
+                }
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) acc[i][nt] = mfma32(ah[i], b[nt], acc[i][nt]);
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) acc[i][nt] = mfma32(al[i], b[nt], acc[i][nt]);
+            }
+        }
+    }
+
+    // C layout: acc[i][nt][j] = (token 32 i + 8 (j / 4) + 4 (lane / 32) + j % 4, row 32 nt + lane % 32)
+    if constexpr (KS == 1) {
+        if (!active) return;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = t0 + 32 * i + 8 * (j >> 2) + 4 * kgl + (j & 3);
+                if (t < a.T)
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) tern_store(a, m, mi, t, rbase + 32 * nt + n, acc[i][nt][j]);
+            }
+    } else {
+        // partial tiles of the KS waves (one row group, MT = 1): red[ks][32 tokens][64 rows]
+        float* red = reinterpret_cast<float*>(lds);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int tl = 8 * (j >> 2) + 4 * kgl + (j & 3);
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) red[(ks * 32 + tl) * 64 + 32 * nt + n] = acc[0][nt][j];
+        }
+        __syncthreads();
+        if (!active) return;
+        // thread p sums outputs p, p + 256, ... of the 32 x 64 tile in ks order
+        for (int p = threadIdx.x; p < 32 * 64; p += 64 * KS) {
+            const int tl = p >> 6, col = p & 63;
+            if (t0 + tl >= a.T) continue;
+            float v = red[p];
+#pragma unroll
+            for (int k2 = 1; k2 < KS; ++k2) v += red[k2 * 32 * 64 + p];
+            tern_store(a, m, mi, t0 + tl, rbase + col, v);
+        }
+    }
+}
+
+}  // namespace bn

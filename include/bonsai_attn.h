@@ -41,7 +41,7 @@ extern "C" {
 #endif
 
 #define BN_HEAD_DIM 256
-#define BN_ABI_VERSION 2
+#define BN_ABI_VERSION 3
 
 typedef enum bn_status {
     BN_OK = 0,
@@ -178,6 +178,34 @@ typedef struct bn_kv_state {
 #define BN_KV_SECTION_VERSION 1u
 #define BN_KV_SECTION_HEADER 24
 
+/* A ternary packed linear (kernels/qmv.glsl:1-2; model.rs:133-139 Lin): row n of W is k / 16 uint32 words, word j
+ * holding the codes of columns 16j + e at bits [2e, 2e + 2); one fp16 scale per 128 columns at s[n * k/128 + c/128];
+ * the weight of column c is scale * (code - 1). */
+typedef struct bn_ternary_mat {
+    const uint32_t* w;       /* [o][k / 16], 16-byte aligned */
+    const uint16_t* s;       /* [o][k / 128] fp16 */
+    float* y;                /* output: token t's o values at y + t * y_ts */
+    const uint16_t* lora_b;  /* LoRA up projection B [o][lora_r] fp16 (alpha / r folded in, lora.rs:140-146), or
+                              * NULL: no adapter on this matrix (the reference's zero B) */
+    uint32_t o;              /* rows: a multiple of 64 */
+    int64_t y_ts;
+} bn_ternary_mat;
+
+/* Up to three matmuls sharing one input (the q/k/v projections of an attention layer; o_proj alone with
+ * add = 1): y_i[t] (+)= x[t] W_i^T, then + lora_b_i . u (model.rs:455-596 qmm_lora / qmm / qmm_multi). */
+typedef struct bn_ternary_args {
+    uint32_t T;              /* tokens (1 = decode step, 2..16 = verify rows, more = prefill) */
+    uint32_t k;              /* input width: a multiple of 128 */
+    const float* x;          /* token t at x + t * x_ts (16-byte aligned, x_ts a multiple of 4) */
+    int64_t x_ts;
+    uint32_t n_mats;         /* 1..3 */
+    uint32_t add;            /* 1: y += result (o_proj into the residual stream, model.rs:893) */
+    bn_ternary_mat mat[3];
+    const float* lora_u;     /* LoRA down projections: token t, matrix i at lora_u + t * lora_us + i * lora_r */
+    int64_t lora_us;
+    uint32_t lora_r;         /* LoRA rank (0: none) */
+} bn_ternary_args;
+
 /* ---- context ---------------------------------------------------------------------------------- */
 bn_status bn_ctx_create(int device, bn_ctx** out);
 void bn_ctx_destroy(bn_ctx* ctx);
@@ -248,6 +276,14 @@ bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a)
  * a->v_new are NULL and a->flags is 0. p->q is needed only for T > 16; otherwise it may be NULL and is not
  * written. Same workspace as bn_attn_forward. */
 bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, const bn_attn_args* a);
+
+/* ---- ternary projections either side of the attention call ------------------------------------------ */
+bn_status bn_ternary_check(const bn_ternary_args* a);
+/* y = (add ? y : 0) + x W^T (+ LoRA) for each matrix (model.rs:455-596: qmm_multi / qmv4 for one token, qmvr,
+ * qmvx and qmm3 for more; kernels.metal:431-500 qmm, 664-709 qmvxm). Results are fp32 sums of exact products up to
+ * x's 2^-22 relative split error (the reference computes in fp32), identical from call to call. y must not overlap
+ * x, W or another matrix's y. */
+bn_status bn_ternary_matmul(bn_ctx* ctx, bn_stream stream, const bn_ternary_args* a);
 
 #ifdef __cplusplus
 }

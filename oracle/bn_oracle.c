@@ -388,3 +388,34 @@ void bn_or_gate_rotate(const float* attn, const float* qp, const float* signs, f
         }
     }
 }
+
+/* qmm3.comp:16-40: the weight of (n, k) is ((float)code - 1.0) * scale (qmm3.comp:32, exact in fp32), each output
+ * sums x * w over k in order (qmm3.comp:34-38), then store_post (qmv.glsl:10-15): y = (add ? y + v : v) +
+ * lora_acc, lora_acc = sum_j u[j] * B[n][j] in j order (qmv.glsl:4-8). */
+void bn_or_ternary(const uint32_t* W, const uint16_t* S, const float* X, int64_t x_ts, float* Y, int64_t y_ts,
+                   int T, int K, int O, int add, const uint16_t* B, const float* U, int64_t u_ts, int lr, int nthreads) {
+    const int kw = K / 16, kg = K / 128;
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < O; n++) {
+        float* w = (float*)malloc((size_t)K * sizeof(float));
+        for (int k = 0; k < K; k++) {
+            const uint32_t code = (W[(size_t)n * kw + k / 16] >> (2 * (k % 16))) & 3u;
+            w[k] = ((float)code - 1.0f) * bn_or_f16_to_f32(S[(size_t)n * kg + k / 128]);
+        }
+        for (int t = 0; t < T; t++) {
+            const float* x = X + (size_t)t * x_ts;
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) acc = fmaf(x[k], w[k], acc);
+            float* y = Y + (size_t)t * y_ts + n;
+            float yv = add ? *y + acc : acc;
+            if (B && lr > 0) {
+                float la = 0.0f;
+                for (int j = 0; j < lr; j++) la = fmaf(U[(size_t)t * u_ts + j], bn_or_f16_to_f32(B[(size_t)n * lr + j]), la);
+                yv = yv + la;
+            }
+            *y = yv;
+        }
+        free(w);
+    }
+}

@@ -49,6 +49,8 @@ def lib():
     L.bn_or_sincos.restype = None
     L.bn_or_gate_rotate.argtypes = [P, P, P, P, I, I]
     L.bn_or_gate_rotate.restype = None
+    L.bn_or_ternary.argtypes = [P, P, P, I64, P, I64, I, I, I, I, P, P, I64, I, I]
+    L.bn_or_ternary.restype = None
     _lib = L
     return L
 
@@ -156,3 +158,21 @@ def gate_rotate(attn, qp, signs):
     lib().bn_or_gate_rotate(_p(np.ascontiguousarray(attn, np.float32)), _p(np.ascontiguousarray(qp, np.float32)),
                             _p(np.ascontiguousarray(signs, np.float32)), _p(xr), T, W)
     return xr
+
+
+def ternary(w, s, x, y=None, lora_b=None, lora_u=None, nthreads=0):
+    """One ternary linear (qmm3.comp order): w uint32 [O][K/16], s uint16 fp16 [O][K/128], x float32 [T][K];
+    y (float32 [T][O]) is added to when given (add = 1) and returned; lora_b uint16 [O][r], lora_u float32 [T][r]."""
+    w = np.ascontiguousarray(w, np.uint32)
+    s = np.ascontiguousarray(s, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    T, K = x.shape
+    O = w.shape[0]
+    assert w.shape == (O, K // 16) and s.shape == (O, K // 128)
+    add = y is not None
+    out = np.ascontiguousarray(y, np.float32).copy() if add else np.empty((T, O), np.float32)
+    lr = 0 if lora_b is None else lora_b.shape[1]
+    b = None if lora_b is None else np.ascontiguousarray(lora_b, np.uint16)
+    u = None if lora_u is None else np.ascontiguousarray(lora_u, np.float32)
+    lib().bn_or_ternary(_p(w), _p(s), _p(x), K, _p(out), O, T, K, O, int(add), _p(b), _p(u), lr, lr, nthreads)
+    return out

@@ -34,7 +34,7 @@ def test_header_and_binding_agree():
 def test_library_exports_every_declared_symbol(lib):
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.bn_abi_version() == 2
+    assert lib.bn_abi_version() == 3
 
 
 def test_status_strings(lib):
@@ -261,3 +261,47 @@ def test_kv_section_format_checks(lib):
     s.len = 101
     assert lib.bn_kv_section_size(s) == 0                                      # len beyond cap
     assert lib.bn_kv_copy(None, None, None, None) == ba.BN_EINVAL
+
+
+def good_ternary(T=8, k=2560, os=(8192, 1024, 1024)):
+    a = ba.TernaryArgs()
+    a.T, a.k = T, k
+    a.x, a.x_ts = 0x900000, k
+    a.n_mats = len(os)
+    for i, o in enumerate(os):
+        base = 0x1000000 * (i + 1)
+        a.mat[i].w, a.mat[i].s, a.mat[i].y = base, base + 0x800000, base + 0xC00000
+        a.mat[i].o, a.mat[i].y_ts = o, o
+    return a
+
+
+@pytest.mark.parametrize("mutate", [
+    lambda a: setattr(a, "k", 2500),                      # not a multiple of 128
+    lambda a: setattr(a, "k", 0),
+    lambda a: setattr(a, "n_mats", 0),
+    lambda a: setattr(a, "n_mats", 4),
+    lambda a: setattr(a, "T", 0),
+    lambda a: setattr(a.mat[1], "o", 1000),               # not a multiple of 64
+    lambda a: setattr(a.mat[0], "w", 0x1000008),          # W not 16-byte aligned
+    lambda a: setattr(a, "x", 0x900004),                  # x not 16-byte aligned
+    lambda a: setattr(a, "x_ts", 2562),                   # row stride not a multiple of 4
+    lambda a: setattr(a, "x_ts", 2048),                   # row stride below k
+    lambda a: setattr(a.mat[2], "y_ts", 512),             # output stride below o
+    lambda a: setattr(a.mat[0], "y", 0),                  # missing output
+    lambda a: setattr(a, "add", 2),
+    lambda a: setattr(a, "lora_r", 8),                    # rank without u
+    lambda a: setattr(a.mat[0], "lora_b", 0x1234000),     # B without a rank
+])
+def test_ternary_check(lib, mutate):
+    assert lib.bn_ternary_check(good_ternary()) == ba.BN_OK
+    assert lib.bn_ternary_check(good_ternary(T=1, k=128, os=(64,))) == ba.BN_OK
+    a = good_ternary()
+    a.lora_u, a.lora_us, a.lora_r = 0xA00000, 48, 16
+    a.mat[1].lora_b = 0x2345000
+    assert lib.bn_ternary_check(a) == ba.BN_OK
+    a = good_ternary()
+    mutate(a)
+    assert lib.bn_ternary_check(a) == ba.BN_EINVAL
+    assert "must" in ba.last_check_error() or "required" in ba.last_check_error() or "given" in ba.last_check_error()
+    assert lib.bn_ternary_check(None) == ba.BN_EINVAL
+    assert lib.bn_ternary_matmul(None, None, None) == ba.BN_EINVAL

@@ -1,0 +1,111 @@
+"""bn_ternary_matmul (the q/k/v/o projections, model.rs:455-596) against the oracle's qmm3-order fp32 matmul.
+
+Every output is within workload.ternary_tolerance of the oracle: 2e-5 of the L2 norm of its K products (fp32 sums in
+another order differ by about 3e-6 of it; a path that rounded x to fp16 would be off by about 2.4e-4), and within the
+north-star max-abs 2e-3. Repeated calls are bit-identical. Cases cover each kernel: the VALU rows kernel (T = 1..4),
+the split-K MFMA kernel (T = 5..32, K split 4 or 2 ways), the 128-token MFMA kernel (T > 32, partly empty token
+and row tiles), one to three matrices sharing x, add into y, LoRA, code 3 and strided rows.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import workload
+from glimpse_language_amd import bonsai_attn as ba
+
+pytestmark = pytest.mark.gpu
+
+
+def make_case(seed, T, K, os, code3=False, lora_r=0, x_pad=0):
+    mats = [workload.ternary_weights(seed + 17 * i, o, K, code3) for i, o in enumerate(os)]
+    x = oracle.normal(seed, 1, (T, K + x_pad))
+    lb = [oracle.f32_to_f16(oracle.normal(seed + i, 2, (o, lora_r))) for i, o in enumerate(os)] if lora_r else None
+    lu = oracle.normal(seed, 3, (T, len(os) * lora_r)) if lora_r else None
+    return mats, x, lb, lu
+
+
+def run_gpu(torch, ctx, mats, x, K, add_y=None, lb=None, lu=None, lora_r=0):
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    xd = dev(x)[:, :K]
+    ys, margs = [], []
+    for i, (w, s, _) in enumerate(mats):
+        y = dev(add_y[i]) if add_y is not None else torch.full((x.shape[0], w.shape[0]), float("nan"), device="cuda")
+        ys.append(y)
+        m = [dev(w.view(np.int32)), dev(s.view(np.int16)), y]
+        if lb is not None:
+            m.append(dev(lb[i].view(np.int16)))
+        margs.append(tuple(m))
+    ba.ternary_matmul(ctx, xd, margs, add=add_y is not None, lora_u=None if lu is None else dev(lu), lora_r=lora_r)
+    torch.cuda.synchronize()
+    return [y.cpu().numpy() for y in ys]
+
+
+def expected(mats, x, K, add_y=None, lb=None, lu=None, lora_r=0):
+    out = []
+    for i, (w, s, _) in enumerate(mats):
+        u = None if lu is None else lu[:, i * lora_r:(i + 1) * lora_r]
+        out.append(oracle.ternary(w, s, x[:, :K], y=None if add_y is None else add_y[i],
+                                  lora_b=None if lb is None else lb[i], lora_u=u))
+    return out
+
+
+def check(got, ref, mats, x, K, what):
+    for i, (g, r) in enumerate(zip(got, ref)):
+        w, s, codes = mats[i]
+        tol = workload.ternary_tolerance(x[:, :K], codes, s)
+        err = np.abs(g.astype(np.float64) - r)
+        bad = np.argwhere(~(err <= tol))
+        assert bad.size == 0, f"{what} mat {i}: {len(bad)} outputs off, first {bad[:3].tolist()}, max err {err.max()}"
+        assert err.max() <= 2e-3
+
+
+# (T, K, output rows per matrix)
+CASES = [
+    (1, 2048, (4096, 512, 512)),   # 2B q/k/v decode step
+    (1, 2560, (2560,)),            # 4B o_proj-sized decode
+    (2, 2048, (512,)), (3, 384, (64, 128)), (4, 1024, (192,)),
+    (5, 2048, (256,)), (8, 2560, (8192, 1024, 1024)),   # 4B verify rows: K split 4 ways
+    (16, 384, (64, 64, 64)),       # K split 2 ways (384 = 2 * 192)
+    (12, 640, (128,)),             # K split 2 ways (640 = 2 * 320, scale groups straddle the halves)
+    (32, 2048, (512,)), (33, 256, (704,)),              # first 128-token tile: partly empty token and row tiles
+    (130, 2048, (512, 128, 128)), (300, 1024, (320,)),
+]
+
+
+@pytest.mark.parametrize("T,K,os", CASES)
+def test_ternary_matches_oracle(gpu, T, K, os):
+    torch, ctx, _ = gpu
+    print(f"ternary T={T} K={K} os={os}", flush=True)
+    mats, x, _, _ = make_case(0x7000 + T + K, T, K, os)
+    got = run_gpu(torch, ctx, mats, x, K)
+    check(got, expected(mats, x, K), mats, x, K, f"T={T} K={K}")
+    again = run_gpu(torch, ctx, mats, x, K)
+    assert all(np.array_equal(a, b) for a, b in zip(got, again)), "repeat call not bit-identical"
+
+
+@pytest.mark.parametrize("T", [1, 3, 8, 40])
+def test_ternary_add_lora_code3_strided(gpu, T):
+    torch, ctx, _ = gpu
+    K, os, r = 512, (128, 64), 6
+    print(f"ternary add/lora T={T}", flush=True)
+    mats, x, lb, lu = make_case(0x7100 + T, T, K, os, code3=True, lora_r=r, x_pad=12)
+    y0 = [oracle.normal(0x7100 + T, 5 + i, (T, o)) for i, o in enumerate(os)]
+    got = run_gpu(torch, ctx, mats, x, K, add_y=y0, lb=lb, lu=lu, lora_r=r)
+    check(got, expected(mats, x, K, add_y=y0, lb=lb, lu=lu, lora_r=r), mats, x, K, f"add/lora T={T}")
+
+
+def test_ternary_one_matrix_without_lora(gpu):
+    """With a LoRA rank set, a matrix with lora_b = NULL gets no up projection (the reference's zero B)."""
+    torch, ctx, _ = gpu
+    T, K, os, r = 2, 256, (64, 64), 4
+    mats, x, lb, lu = make_case(0x7200, T, K, os, lora_r=r)
+    lb_none = [lb[0], None]
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    ys = [torch.zeros((T, o), device="cuda") for o in os]
+    margs = [(dev(mats[0][0].view(np.int32)), dev(mats[0][1].view(np.int16)), ys[0], dev(lb[0].view(np.int16))),
+             (dev(mats[1][0].view(np.int32)), dev(mats[1][1].view(np.int16)), ys[1])]
+    ba.ternary_matmul(ctx, dev(x), margs, lora_u=dev(lu), lora_r=r)
+    torch.cuda.synchronize()
+    ref = [oracle.ternary(mats[0][0], mats[0][1], x, lora_b=lb_none[0], lora_u=lu[:, :r]),
+           oracle.ternary(mats[1][0], mats[1][1], x)]
+    check([y.cpu().numpy() for y in ys], ref, mats, x, K, "lora_b NULL")

@@ -326,3 +326,83 @@ def test_argmax_check_flags_flips_and_excuses_only_ties():
     out[1] = (tie_ref[1].reshape(-1) - 1e-6 * d).reshape(H, 256)
     bad, ties = workload.argmax_mismatches(out, tie_ref, R)
     assert 1 in ties and len(bad) == 0
+
+
+# ---------------------------------------------------------------------------------------------------------
+# Ternary linears (qmm3.comp order). Pinned by words written out by hand (the bit layout of qmv.glsl:1-2), a
+# decoder that reads the codes out of each word's binary string, one-hot inputs (the column -> scale group map)
+# and the LoRA / add closed forms.
+def test_ternary_known_words():
+    K, O = 128, 64
+    w = np.full((O, K // 16), 0x55555555, np.uint32)  # every code 1: weight 0
+    w[0, 0] = 0x00000000  # row 0, columns 0..15: code 0, weight -s
+    w[1, 0] = 0xAAAAAAAA  # row 1, columns 0..15: code 2, weight +s
+    w[2, 0] = 0x55555559  # row 2: column 0 code 1 (0), column 1 code 2 (+s), columns 2..15 code 1
+    w[3, 7] = 0xD5555555  # row 3: column 127 = 16*7 + 15 has code 3 (+2s); bits 30-31 = 0b11
+    w[4, 3] = 0x55555554  # row 4: column 48 code 0 (-s)
+    s = oracle.f32_to_f16(np.full((O, 1), 0.5, np.float32))
+    x = np.arange(1, K + 1, dtype=np.float32)[None, :]  # x[k] = k + 1
+    y = oracle.ternary(w, s, x)[0]
+    assert y[0] == -0.5 * np.sum(np.arange(1, 17))
+    assert y[1] == 0.5 * np.sum(np.arange(1, 17))
+    assert y[2] == 0.5 * 2.0
+    assert y[3] == 2 * 0.5 * 128.0
+    assert y[4] == -0.5 * 49.0
+    assert not y[5:].any()
+
+
+def decode_by_string(w, s):
+    """float64 weights, reading code e of each word from its 32-character binary string (bits 2e, 2e+1)."""
+    O, kw = w.shape
+    sf = oracle.f16_to_f32(s).astype(np.float64)
+    out = np.empty((O, kw * 16))
+    for n in range(O):
+        for j in range(kw):
+            b = format(int(w[n, j]), "032b")
+            for e in range(16):
+                code = int(b[30 - 2 * e:32 - 2 * e], 2)
+                out[n, 16 * j + e] = (code - 1) * sf[n, (16 * j + e) // 128]
+    return out
+
+
+def test_ternary_string_decoder():
+    K, O, T = 256, 64, 3
+    w, s, codes = workload.ternary_weights(0x7E01, O, K, code3=True)
+    x = oracle.normal(0x7E01, 1, (T, K))
+    ref = x.astype(np.float64) @ decode_by_string(w, s).T
+    got = oracle.ternary(w, s, x)
+    assert np.all(np.abs(got - ref) <= workload.ternary_tolerance(x, codes, s))
+    # pack_codes is the inverse of the string decoder's reading
+    dec = decode_by_string(w, oracle.f32_to_f16(np.ones((O, K // 128), np.float32)))
+    assert np.array_equal(dec + 1, codes.astype(np.float64))
+
+
+def test_ternary_scale_groups_one_hot():
+    """x = e_k selects column k: y[n] = s[n, k // 128] * (code[n, k] - 1) exactly."""
+    K, O = 384, 64
+    w, s, codes = workload.ternary_weights(0x7E02, O, K, code3=True)
+    cols = [0, 1, 15, 16, 127, 128, 200, 255, 256, 383]
+    x = np.zeros((len(cols), K), np.float32)
+    x[np.arange(len(cols)), cols] = 1.0
+    got = oracle.ternary(w, s, x)
+    sf = oracle.f16_to_f32(s)
+    for i, k in enumerate(cols):
+        assert np.array_equal(got[i], sf[:, k // 128] * (codes[:, k].astype(np.float32) - 1.0))
+
+
+def test_ternary_add_and_lora():
+    K, O, T, r = 128, 64, 2, 5
+    w, s, codes = workload.ternary_weights(0x7E03, O, K)
+    x = oracle.normal(0x7E03, 1, (T, K))
+    y0 = oracle.normal(0x7E03, 2, (T, O))
+    b = oracle.f32_to_f16(oracle.normal(0x7E03, 3, (O, r)))
+    u = oracle.normal(0x7E03, 4, (T, r))
+    plain = oracle.ternary(w, s, x)
+    both = oracle.ternary(w, s, x, y=y0, lora_b=b, lora_u=u)
+    lora = u.astype(np.float64) @ oracle.f16_to_f32(b).astype(np.float64).T
+    assert np.max(np.abs(both - (y0 + plain + lora))) < 1e-5
+    # all-zero codes: y = -s * sum(x) per scale group
+    wz = np.zeros_like(w)
+    got = oracle.ternary(wz, s, x)
+    sf = oracle.f16_to_f32(s).astype(np.float64)
+    assert np.max(np.abs(got - (-sf[:, 0][None, :] * x.astype(np.float64).sum(1)[:, None]))) < 1e-4

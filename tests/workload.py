@@ -72,3 +72,31 @@ def argmax_mismatches(out, ref, R):
     tie = (top2[:, 1] - top2[:, 0]) < TIE_REL * np.abs(top2[:, 1])
     diff = np.argmax(po, axis=1) != np.argmax(pr, axis=1)
     return np.nonzero(diff & ~tie)[0], np.nonzero(tie)[0]
+
+
+# ---- ternary projections ------------------------------------------------------------------------------------
+def ternary_weights(seed, O, K, code3=False):
+    """Packed ternary weights: codes uniform in {0, 1, 2} (and 3 when code3, weight 2 * scale), 16 per uint32 with
+    code e of word j (column 16j + e) at bits [2e, 2e + 2); fp16 scales |N(0,1)| * 0.02 + 0.005 per 128 columns."""
+    u = oracle.normal(seed, 7, (O, K))
+    hi = 4 if code3 else 3
+    codes = np.floor((np.tanh(u) * 0.5 + 0.5) * hi).clip(0, hi - 1).astype(np.uint32)
+    w = pack_codes(codes)
+    s = oracle.f32_to_f16(np.abs(oracle.normal(seed, 8, (O, K // 128))) * 0.02 + 0.005)
+    return w, s, codes
+
+
+def pack_codes(codes):
+    """[O, K] codes 0..3 -> [O, K/16] uint32."""
+    O, K = codes.shape
+    c = codes.reshape(O, K // 16, 16).astype(np.uint32)
+    return np.bitwise_or.reduce(c << (2 * np.arange(16, dtype=np.uint32)), axis=2).astype(np.uint32)
+
+
+def ternary_tolerance(x, codes, s):
+    """Per-output bound for comparing two fp32 evaluations of x W^T: 2e-5 * ||(x_k w_k)_k||_2 + 1e-6. fp32 sums of K
+    products differ by about 2^-24 sqrt(K) of that norm (3e-6 at K = 2560); rounding x to fp16 alone would move them
+    by about 2^-12 of it (2.4e-4), so a path that dropped x's low half fails."""
+    w = (codes.astype(np.float64) - 1.0) * np.repeat(oracle.f16_to_f32(s).astype(np.float64), 128, axis=1)
+    n2 = (x.astype(np.float64) ** 2) @ (w ** 2).T
+    return 2e-5 * np.sqrt(n2) + 1e-6
