@@ -26,7 +26,8 @@ EXPORTS = (
     "bn_workspace_clear", "bn_attn_forward", "bn_attn_decode", "bn_attn_verify", "bn_attn_prefill",
     "bn_attn_append", "bn_attn_decode_ragged", "bn_prep_check", "bn_rotate_check", "bn_attn_prep",
     "bn_gate_rotate", "bn_attn_layer", "bn_layer_check", "bn_kv_copy", "bn_kv_section_size", "bn_kv_section_save",
-    "bn_kv_section_check", "bn_kv_section_load", "bn_ternary_check", "bn_ternary_matmul",
+    "bn_kv_section_check", "bn_kv_section_load", "bn_ternary_check", "bn_ternary_matmul", "bn_norm_check",
+    "bn_norm_rotate",
 )
 KV_SECTION_MAGIC = b"BNKVF16\0"
 KV_SECTION_HEADER = 24
@@ -108,6 +109,14 @@ class TernaryArgs(ctypes.Structure):
     ]
 
 
+class NormArgs(ctypes.Structure):
+    _fields_ = [
+        ("T", ctypes.c_uint32), ("d", ctypes.c_uint32), ("h", ctypes.c_void_p), ("h_ts", ctypes.c_int64),
+        ("w", ctypes.c_void_p), ("signs", ctypes.c_void_p), ("xn", ctypes.c_void_p), ("xn_ts", ctypes.c_int64),
+        ("xr", ctypes.c_void_p), ("xr_ts", ctypes.c_int64),
+    ]
+
+
 def load(path=LIB_PATH):
     """Loads the HIP library (raises if it has not been built)."""
     global _lib
@@ -170,6 +179,10 @@ def load(path=LIB_PATH):
     lib.bn_ternary_check.restype = ctypes.c_int
     lib.bn_ternary_matmul.argtypes = [P, P, ctypes.POINTER(TernaryArgs)]
     lib.bn_ternary_matmul.restype = ctypes.c_int
+    lib.bn_norm_check.argtypes = [ctypes.POINTER(NormArgs)]
+    lib.bn_norm_check.restype = ctypes.c_int
+    lib.bn_norm_rotate.argtypes = [P, P, ctypes.POINTER(NormArgs)]
+    lib.bn_norm_rotate.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -504,3 +517,22 @@ def ternary_args(x, mats, add=False, lora_u=None, lora_r=0):
 def ternary_matmul(ctx, x, mats, add=False, lora_u=None, lora_r=0, stream=None):
     """bn_ternary_matmul: y_i (+)= x W_i^T (+ LoRA) for each (w, s, y[, lora_b]) in mats; y tensors are written."""
     ctx.call("bn_ternary_matmul", ternary_args(x, mats, add, lora_u, lora_r), stream)
+
+
+def norm_args(h, w, signs, xr, xn=None):
+    a = NormArgs()
+    a.T, a.d = h.shape[0], h.shape[1]
+    a.h, a.h_ts = _ptr(h), h.stride(0)
+    a.w, a.signs = _ptr(w), _ptr(signs)
+    a.xn, a.xn_ts = _ptr(xn), xn.stride(0) if xn is not None else 0
+    a.xr, a.xr_ts = _ptr(xr), xr.stride(0)
+    return a
+
+
+def norm_rotate(ctx, h, w, signs, xr=None, xn=None, stream=None):
+    """norm_rotate: xr = FWHT-512(signs * rmsnorm(h) * w) / sqrt(512) per block (returned); xn = rmsnorm(h) * w."""
+    import torch
+    if xr is None:
+        xr = torch.empty_like(h)
+    ctx.call("bn_norm_rotate", norm_args(h, w, signs, xr, xn), stream)
+    return xr

@@ -572,6 +572,20 @@ bn_status check_ternary(const bn_ternary_args* a, char* why) {
     return BN_OK;
 }
 
+bn_status check_norm(const bn_norm_args* a, char* why) {
+    if (!a) return set_err(why, BN_EINVAL, "args is NULL");
+    if (a->T < 1 || a->T > (1u << 30)) return set_err(why, BN_EINVAL, "T must be in 1..2^30");
+    if (a->d < 512 || (a->d & 511) || a->d > (1u << 16) * 512u)
+        return set_err(why, BN_EINVAL, "d must be a multiple of 512 (d=%u)", a->d);
+    if (!a->h || !a->w || !a->signs || !a->xr) return set_err(why, BN_EINVAL, "h, w, signs and xr are required");
+    if (!aligned16(a->h) || !aligned16(a->w) || !aligned16(a->signs) || !aligned16(a->xr) || !aligned16(a->xn))
+        return set_err(why, BN_EINVAL, "h, w, signs, xn and xr must be 16-byte aligned");
+    if ((a->h_ts & 3) || (a->xr_ts & 3) || (a->xn && (a->xn_ts & 3)) ||
+        (a->T > 1 && (a->h_ts < (int64_t)a->d || a->xr_ts < (int64_t)a->d || (a->xn && a->xn_ts < (int64_t)a->d))))
+        return set_err(why, BN_EINVAL, "row strides must be multiples of 4, at least d");
+    return BN_OK;
+}
+
 // K split of the small-T MFMA kernel: 4 ways when each quarter of K is whole 64-column chunks, else 2 (k is a
 // multiple of 128)
 int tern_ksplit(uint32_t k) { return (k % (4 * bn::TERN_KC) == 0) ? 4 : 2; }
@@ -623,8 +637,8 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
     const int row_tiles = (int)ceil_div(rows, 256);
     const int64_t blocks = (int64_t)row_tiles * ceil_div(a->T, 32 * MT);
     if (blocks > INT32_MAX) return set_err(ctx->err, BN_EINVAL, "T * rows too large for one launch");
-    hipLaunchKernelGGL((bn::tern_mfma_kernel<MT, 1, 4, BN_TERN_PF_OCC>), dim3((unsigned)blocks), dim3(256), 0, st, t,
-                       row_tiles);
+    hipLaunchKernelGGL((bn::tern_mfma_kernel<MT, 1, 4, BN_TERN_PF_OCC, BN_TERN_PF_KC>), dim3((unsigned)blocks),
+                       dim3(256), 0, st, t, row_tiles);
     return launched(ctx, "tern_mfma_kernel (prefill)");
 }
 
@@ -918,6 +932,27 @@ bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, co
 }
 
 bn_status bn_ternary_check(const bn_ternary_args* a) { return check_ternary(a, g_check_err); }
+
+bn_status bn_norm_check(const bn_norm_args* a) { return check_norm(a, g_check_err); }
+
+bn_status bn_norm_rotate(bn_ctx* ctx, bn_stream stream, const bn_norm_args* a) {
+    if (!ctx) return BN_EINVAL;
+    bn_status s = check_norm(a, ctx->err);
+    if (s) return s;
+    bn::NormRotateArgs n{};
+    n.h = a->h;
+    n.h_ts = a->h_ts;
+    n.w = a->w;
+    n.signs = a->signs;
+    n.xn = a->xn;
+    n.xn_ts = a->xn_ts;
+    n.xr = a->xr;
+    n.xr_ts = a->xr_ts;
+    n.T = (int)a->T;
+    n.D = (int)a->d;
+    hipLaunchKernelGGL(bn::norm_rotate_kernel, dim3(a->T, a->d / 512), dim3(64), 0, (hipStream_t)stream, n);
+    return launched(ctx, "norm_rotate_kernel");
+}
 
 bn_status bn_ternary_matmul(bn_ctx* ctx, bn_stream stream, const bn_ternary_args* a) {
     if (!ctx) return BN_EINVAL;

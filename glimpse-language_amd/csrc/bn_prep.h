@@ -177,4 +177,59 @@ __global__ __launch_bounds__(64) void rotate_kernel(RotateArgs a) {
             f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512;
 }
 
+struct NormRotateArgs {
+    const float* h;          // hidden rows: element t*h_ts + e
+    int64_t h_ts;
+    const float* w;          // [D] RMSNorm weight
+    const float* signs;      // [D], +-1
+    float* xn;               // normed rows (element t*xn_ts + e), or null
+    int64_t xn_ts;
+    float* xr;               // rotated rows: element t*xr_ts + e
+    int64_t xr_ts;
+    int T, D;                // D a multiple of 512
+};
+
+// norm_rotate (kernels/norm_rotate.comp:10-33): xn = h * (1 / sqrt(sum h^2 / D + 1e-6)) * w, xr = FWHT-512(signs *
+// xn) / sqrt(512) per 512-element block. Grid (T, D / 512) x one wave; each wave sums the squares of its whole row
+// (the row is read from L2 by every block of it, which keeps the blocks independent) while its own block's 512
+// elements load, in the lane layout of rotate_kernel.
+__global__ __launch_bounds__(64) void norm_rotate_kernel(NormRotateArgs a) {
+    const int t = blockIdx.x, lane = threadIdx.x, b = blockIdx.y;
+    const float* x = a.h + t * a.h_ts;
+    f4 xv[2], wv[2], sv[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int e = 512 * b + 256 * i + 4 * lane;
+        xv[i] = *reinterpret_cast<const f4*>(x + e);
+        wv[i] = *reinterpret_cast<const f4*>(a.w + e);
+        sv[i] = *reinterpret_cast<const f4*>(a.signs + e);
+    }
+    float ss = 0.0f;
+    for (int e = 4 * lane; e < a.D; e += 256) {
+        const f4 v = *reinterpret_cast<const f4*>(x + e);
+        ss = fmaf(v[0], v[0], ss);
+        ss = fmaf(v[1], v[1], ss);
+        ss = fmaf(v[2], v[2], ss);
+        ss = fmaf(v[3], v[3], ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const float r = 1.0f / sqrtf(ss / (float)a.D + 1e-6f);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        f4 n;
+#pragma unroll
+        for (int c = 0; c < 4; c++) n[c] = (xv[i][c] * r) * wv[i][c];
+        if (a.xn) *reinterpret_cast<f4*>(a.xn + t * a.xn_ts + 512 * b + 256 * i + 4 * lane) = n;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[4 * i + c] = n[c] * sv[i][c];
+    }
+    fwht512_wave(v, lane);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        *reinterpret_cast<f4*>(a.xr + t * a.xr_ts + 512 * b + 256 * i + 4 * lane) =
+            f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512;
+}
+
 }  // namespace bn

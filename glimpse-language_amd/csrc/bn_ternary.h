@@ -187,6 +187,9 @@ constexpr int TERN_KC = 64;  // k per staged chunk (4 MFMA k-steps of 16)
 #ifndef BN_TERN_PF_OCC
 #define BN_TERN_PF_OCC 2
 #endif
+#ifndef BN_TERN_PF_KC
+#define BN_TERN_PF_KC 64
+#endif
 
 // 8 codes of word `wd` as fp16 (code - 1) * s: slots 2i, 2i+1 = codes 4kg + i, 12... see the A layout below.
 // wd2 = kg ? wd : wd << 8 puts the lane's codes (4kg + i, 8 + 4kg + i) at bits [8 + 2i, ..) and [24 + 2i, ..).
@@ -221,14 +224,16 @@ __device__ __forceinline__ void tern_sync() {
 // MT 32-token tiles x 2 32-row tiles per wave; KS waves split K (their partial sums meet in LDS in ks order), RG
 // waves split rows (KS > 1 only with RG = 1). Block: 64 * KS * RG threads, 32 * MT tokens x 64 * RG rows.
 //
-// A layout in LDS, per k-split group: hi[4 q][2 kg][32 MT m][8 slots] fp16, then lo the same. Slot i of (q, kg, m)
+// A layout in LDS, per k-split group: hi[KC / 16 q][2 kg][32 MT m][8 slots] fp16, then lo the same. Slot i of (q, kg, m)
 // holds x[m][k0 + 16q + 4kg + 8(i & 1) + (i >> 1)], the k order tern_decode8 gives the B operand, so each lane's A
 // operand (m = lane % 32, kg = lane / 32) is one 16-byte LDS read.
-template <int MT, int KS, int RG, int OCC = 1>
+template <int MT, int KS, int RG, int OCC = 1, int KC = TERN_KC>
 __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row_tiles) {
+    constexpr int NQ = KC / 16;        // MFMA k-steps per chunk
+    static_assert(KC == 64 || KC == 128, "a chunk lies inside one 128-column scale group");
     static_assert(KS * RG <= 4 && (KS == 1 || (RG == 1 && MT == 1)), "split-K blocks are one token tile, one row group");
     constexpr int BM = 32 * MT;        // tokens per block
-    constexpr int GROUP_H = 2 * 8 * BM * 8;  // fp16 per k-split group (hi and lo): 4 q * 2 kg * BM * 8 * 2
+    constexpr int GROUP_H = 2 * NQ * 2 * BM * 8;  // fp16 per k-split group (hi and lo): NQ q * 2 kg * BM * 8 * 2
     // one buffer, two syncs per chunk: a second buffer costs registers and occupancy (3 -> 2 waves per SIMD for
     // the prefill shape) and measured slower on MI355X
     __shared__ __attribute__((aligned(16))) _Float16 lds[KS * GROUP_H];
@@ -247,10 +252,10 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
     const TernMat m = tern_mat(a, mi);
 
     const int K = a.K, kw = K >> 4, kg = K >> 7;
-    const int klen = K / KS, kbase = ks * klen, nchunk = klen / TERN_KC;
+    const int klen = K / KS, kbase = ks * klen, nchunk = klen / KC;
 
-    // staging: group thread gt of 64 * RG takes units u = gt + i * 64 * RG, u = (m * 4 + q) * 2 + kgu
-    constexpr int GT = 64 * RG, UPT = 8 * BM / GT;
+    // staging: group thread gt of 64 * RG takes units u = gt + i * 64 * RG, u = (m * NQ + q) * 2 + kgu
+    constexpr int GT = 64 * RG, UPT = 2 * NQ * BM / GT;
     const int gt = rg * 64 + lane;
     _Float16* glds = lds + ks * GROUP_H;
     f4 xa[UPT], xb[UPT];
@@ -258,10 +263,10 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
             const int u = gt + i * GT;
-            const int mm = u >> 3, q = (u >> 1) & 3, kgu = u & 1;
+            const int mm = u / (2 * NQ), q = (u >> 1) % NQ, kgu = u & 1;
             // token rows past T are neither loaded nor staged: their A rows only feed outputs that are not stored
             if (t0 + mm < a.T) {
-                const float* p = a.x + (int64_t)(t0 + mm) * a.x_ts + kbase + c * TERN_KC + 16 * q + 4 * kgu;
+                const float* p = a.x + (int64_t)(t0 + mm) * a.x_ts + kbase + c * KC + 16 * q + 4 * kgu;
                 xa[i] = *reinterpret_cast<const f4*>(p);
                 xb[i] = *reinterpret_cast<const f4*>(p + 8);
             }
@@ -271,7 +276,7 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
             const int u = gt + i * GT;
-            const int mm = u >> 3, q = (u >> 1) & 3, kgu = u & 1;
+            const int mm = u / (2 * NQ), q = (u >> 1) % NQ, kgu = u & 1;
             if (t0 + mm >= a.T) continue;
             h8 hi, lo;
 #pragma unroll
@@ -283,7 +288,7 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
             }
             const int off = ((q * 2 + kgu) * BM + mm) * 8;
             *reinterpret_cast<h8*>(glds + off) = hi;
-            *reinterpret_cast<h8*>(glds + 8 * BM * 8 + off) = lo;
+            *reinterpret_cast<h8*>(glds + 2 * NQ * BM * 8 + off) = lo;
         }
     };
 
@@ -297,10 +302,12 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
         wrow[nt] = m.w + row * kw + kbase / 16;
         srow[nt] = m.s + row * kg;
     }
-    u4 wv[2];
+    u4 wv[2][NQ / 4];
     auto load_w = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) wv[nt] = *reinterpret_cast<const u4*>(wrow[nt] + c * (TERN_KC / 16));
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int h = 0; h < NQ / 4; ++h) wv[nt][h] = *reinterpret_cast<const u4*>(wrow[nt] + c * (KC / 16) + 4 * h);
     };
 
     f16x acc[MT][2];
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
     auto scales = [&](int c, h2 (&s2)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            const _Float16 sv = active ? __builtin_bit_cast(_Float16, srow[nt][(kbase + c * TERN_KC) >> 7]) : (_Float16)0;
+            const _Float16 sv = active ? __builtin_bit_cast(_Float16, srow[nt][(kbase + c * KC) >> 7]) : (_Float16)0;
             s2[nt] = h2{sv, sv};
         }
     };
@@ -324,7 +331,12 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
     for (int c = 0; c < nchunk; ++c) {
         tern_sync<KS>();  // the previous chunk's A reads are done
         store_x();
-        u4 wcur[2] = {wv[0], wv[1]};
+        u4 wcur[2][NQ / 4];
+#pragma unroll
+        for (int h = 0; h < NQ / 4; ++h) {
+            wcur[0][h] = wv[0][h];
+            wcur[1][h] = wv[1][h];
+        }
         h2 s2[2];
         scales(c, s2);
         tern_sync<KS>();
@@ -334,16 +346,16 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
         }
         if (active) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < NQ; ++q) {
                 h8 b[2];
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) b[nt] = tern_decode8(wcur[nt][q] << shift, s2[nt]);
+                for (int nt = 0; nt < 2; ++nt) b[nt] = tern_decode8(wcur[nt][q >> 2][q & 3] << shift, s2[nt]);
                 h8 ah[MT], al[MT];
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
                     const int off = ((q * 2 + kgl) * BM + 32 * i + n) * 8;
                     ah[i] = *reinterpret_cast<const h8*>(glds + off);
-                    al[i] = *reinterpret_cast<const h8*>(glds + 8 * BM * 8 + off);
+                    al[i] = *reinterpret_cast<const h8*>(glds + 2 * NQ * BM * 8 + off);
                 }
 #pragma unroll
                 for (int i = 0; i < MT; ++i)

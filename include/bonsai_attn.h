@@ -206,6 +206,21 @@ typedef struct bn_ternary_args {
     uint32_t lora_r;         /* LoRA rank (0: none) */
 } bn_ternary_args;
 
+/* norm_rotate (kernels/norm_rotate.comp:3-33, model.rs:690-707): the input of the q/k/v projections. For each row,
+ * xn = h * (1 / sqrt(sum h^2 / d + 1e-6)) * w and xr = FWHT-512(signs * xn) / sqrt(512) per 512-element block. */
+typedef struct bn_norm_args {
+    uint32_t T;              /* rows */
+    uint32_t d;              /* row width (the model's hidden size): a multiple of 512 */
+    const float* h;          /* row t at h + t * h_ts (16-byte aligned, h_ts a multiple of 4) */
+    int64_t h_ts;
+    const float* w;          /* [d] RMSNorm weight */
+    const float* signs;      /* [d] +-1: the first projection's input signs (model.rs:697, Lin.signs) */
+    float* xn;               /* rmsnorm(h) * w rows (write_xn), or NULL */
+    int64_t xn_ts;
+    float* xr;               /* rotated rows: the projections' x */
+    int64_t xr_ts;
+} bn_norm_args;
+
 /* ---- context ---------------------------------------------------------------------------------- */
 bn_status bn_ctx_create(int device, bn_ctx** out);
 void bn_ctx_destroy(bn_ctx* ctx);
@@ -278,6 +293,10 @@ bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a)
 bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, const bn_attn_args* a);
 
 /* ---- ternary projections either side of the attention call ------------------------------------------ */
+bn_status bn_norm_check(const bn_norm_args* a);
+/* norm_rotate: the q/k/v projections' input from the hidden rows (one launch, one wave per 512-element block). The
+ * reference's fused LoRA down projection (rot.glsl LORA_ROW) is not part of this call: lora_u comes from the caller. */
+bn_status bn_norm_rotate(bn_ctx* ctx, bn_stream stream, const bn_norm_args* a);
 bn_status bn_ternary_check(const bn_ternary_args* a);
 /* y = (add ? y : 0) + x W^T (+ LoRA) for each matrix (model.rs:455-596: qmm_multi / qmv4 for one token, qmvr,
  * qmvx and qmm3 for more; kernels.metal:431-500 qmm, 664-709 qmvxm). Results are fp32 sums of exact products up to

@@ -419,3 +419,46 @@ void bn_or_ternary(const uint32_t* W, const uint16_t* S, const float* X, int64_t
         free(w);
     }
 }
+
+/* norm_rotate.comp:10-33. The sum of squares follows rot.glsl:4-18 (row_ss): 16 partial sums, partial g holding
+ * elements i0 + 32 g + lane of every 512-block i0 per lane (fp32, in i0 order), each summed over its 32 lanes, then
+ * the 16 partials; r = 1 / sqrt(ss / D + EPS) with EPS = 1e-6 (common.glsl); a = (x * r) * w; v = a * sign, the
+ * 512-point FWHT in stage order over index bits 0..8, xr = v * 1/sqrt(512). */
+void bn_or_norm_rotate(const float* h, const float* w, const float* signs, float* xn, float* xr, int T, int D) {
+    const float inv_sqrt512 = 0.044194173824159216f;
+    for (int t = 0; t < T; t++) {
+        const float* x = h + (size_t)t * D;
+        float part[16];
+        for (int g = 0; g < 16; g++) {
+            float lanes[32];
+            for (int l = 0; l < 32; l++) {
+                float acc = 0.0f;
+                for (int i0 = 0; i0 < D; i0 += 512) {
+                    float v = x[i0 + 32 * g + l];
+                    acc += v * v;
+                }
+                lanes[l] = acc;
+            }
+            part[g] = sg_add32(lanes);
+        }
+        float ss = 0.0f;
+        for (int g = 0; g < 16; g++) ss += part[g];
+        const float r = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+        for (int b0 = 0; b0 < D; b0 += 512) {
+            float v[512];
+            for (int i = 0; i < 512; i++) {
+                float a = (x[b0 + i] * r) * w[b0 + i];
+                if (xn) xn[(size_t)t * D + b0 + i] = a;
+                v[i] = a * signs[b0 + i];
+            }
+            for (int m = 1; m < 512; m <<= 1)
+                for (int i = 0; i < 512; i++)
+                    if (!(i & m)) {
+                        float a = v[i], b = v[i + m];
+                        v[i] = a + b;
+                        v[i + m] = a - b;
+                    }
+            for (int i = 0; i < 512; i++) xr[(size_t)t * D + b0 + i] = v[i] * inv_sqrt512;
+        }
+    }
+}

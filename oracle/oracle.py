@@ -49,6 +49,8 @@ def lib():
     L.bn_or_sincos.restype = None
     L.bn_or_gate_rotate.argtypes = [P, P, P, P, I, I]
     L.bn_or_gate_rotate.restype = None
+    L.bn_or_norm_rotate.argtypes = [P, P, P, P, P, I, I]
+    L.bn_or_norm_rotate.restype = None
     L.bn_or_ternary.argtypes = [P, P, P, I64, P, I64, I, I, I, I, P, P, I64, I, I]
     L.bn_or_ternary.restype = None
     _lib = L
@@ -176,3 +178,14 @@ def ternary(w, s, x, y=None, lora_b=None, lora_u=None, nthreads=0):
     u = None if lora_u is None else np.ascontiguousarray(lora_u, np.float32)
     lib().bn_or_ternary(_p(w), _p(s), _p(x), K, _p(out), O, T, K, O, int(add), _p(b), _p(u), lr, lr, nthreads)
     return out
+
+
+def norm_rotate(h, w, signs, want_xn=False):
+    """norm_rotate: returns xr [T][D] (and xn when want_xn)."""
+    h = np.ascontiguousarray(h, np.float32)
+    T, Dm = h.shape
+    xr = np.empty_like(h)
+    xn = np.empty_like(h) if want_xn else None
+    lib().bn_or_norm_rotate(_p(h), _p(np.ascontiguousarray(w, np.float32)), _p(np.ascontiguousarray(signs, np.float32)),
+                            _p(xn), _p(xr), T, Dm)
+    return (xr, xn) if want_xn else xr

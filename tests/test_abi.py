@@ -305,3 +305,25 @@ def test_ternary_check(lib, mutate):
     assert "must" in ba.last_check_error() or "required" in ba.last_check_error() or "given" in ba.last_check_error()
     assert lib.bn_ternary_check(None) == ba.BN_EINVAL
     assert lib.bn_ternary_matmul(None, None, None) == ba.BN_EINVAL
+
+
+@pytest.mark.parametrize("mutate", [
+    lambda a: setattr(a, "d", 1000),          # not a multiple of 512
+    lambda a: setattr(a, "T", 0),
+    lambda a: setattr(a, "h", 0x900004),      # misaligned
+    lambda a: setattr(a, "xr", 0),
+    lambda a: setattr(a, "h_ts", 2048),       # stride below d
+    lambda a: setattr(a, "xn_ts", 2561),      # stride not a multiple of 4
+])
+def test_norm_check(lib, mutate):
+    def good():
+        a = ba.NormArgs()
+        a.T, a.d = 4, 2560
+        a.h, a.h_ts, a.w, a.signs = 0x900000, 2560, 0xA00000, 0xB00000
+        a.xn, a.xn_ts, a.xr, a.xr_ts = 0xC00000, 2560, 0xD00000, 2560
+        return a
+    assert lib.bn_norm_check(good()) == ba.BN_OK
+    a = good()
+    mutate(a)
+    assert lib.bn_norm_check(a) == ba.BN_EINVAL
+    assert lib.bn_norm_rotate(None, None, None) == ba.BN_EINVAL

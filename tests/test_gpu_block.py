@@ -1,0 +1,117 @@
+"""A whole attention layer of the runtime on the library's calls, against the oracle's chain of the same steps.
+
+model.rs:690-707 then 815-894: norm_rotate (hidden rows -> the projections' input) -> q/k/v ternary projections ->
+attn_prep + attention + gate + Hadamard rotation (bn_attn_layer) -> o_proj added into the hidden rows. 2B layer
+shapes (hidden 2048, 8 query heads, 2 KV heads). Checked: the new hidden rows within max-abs 2e-3 of the oracle's,
+the appended K and V rows within one fp16 ulp (plus 1e-6). Also bn_norm_rotate alone against the oracle.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import workload
+from test_gpu_prep_rotate import inv_freq
+from glimpse_language_amd import bonsai_attn as ba
+
+pytestmark = pytest.mark.gpu
+D = 256
+HID, H, KV = 2048, 8, 2
+
+
+def assert_f16_rows_close(got, ref):
+    """fp16 rows computed from fp32 projections that were summed in another order: each value within one fp16 ulp of
+    the reference value plus 2e-5, the projections' own tolerance (2e-5 of the norm of their products, about 0.8
+    here) carried through the unit-scale RMS norm (a value near zero can move by many of its tiny ulps)."""
+    g = oracle.f16_to_f32(got)
+    r = oracle.f16_to_f32(ref)
+    ulp = np.spacing(np.abs(r).astype(np.float16)).astype(np.float32)
+    excess = np.abs(g - r) - ulp
+    bad = excess > 2e-5
+    assert not bad.any(), (f"{int(bad.sum())} fp16 values off, first at {np.argwhere(bad)[0].tolist()}, "
+                           f"largest excess over one ulp {excess.max()}")
+
+
+def signs(seed, n):
+    return np.where(oracle.normal(seed, 9, (n,)) > 0, 1.0, -1.0).astype(np.float32)
+
+
+def dev(torch, a):
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    elif a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("T,Dm", [(1, 512), (5, 2048), (300, 2560)])
+def test_norm_rotate_matches_oracle(gpu, T, Dm):
+    torch, ctx, _ = gpu
+    h = oracle.normal(0x7300 + T, 0, (T, Dm)) * np.float32(2.0)
+    w = (1.0 + 0.1 * oracle.normal(0x7300 + T, 1, (Dm,))).astype(np.float32)
+    s = signs(0x7300 + T, Dm)
+    xn = torch.empty((T, Dm), device="cuda")
+    xr = ba.norm_rotate(ctx, dev(torch, h), dev(torch, w), dev(torch, s), xn=xn)
+    torch.cuda.synchronize()
+    ref_xr, ref_xn = oracle.norm_rotate(h, w, s, want_xn=True)
+    assert np.max(np.abs(xn.cpu().numpy() - ref_xn)) <= 1e-5
+    assert np.max(np.abs(xr.cpu().numpy() - ref_xr)) <= 2e-5
+
+
+def block_inputs(seed, T, off):
+    cap = off + T
+    p = np.arange(off, off + T, dtype=np.int32)
+    return dict(
+        h=oracle.normal(seed, 0, (T, HID)),
+        in_w=(1.0 + 0.1 * oracle.normal(seed, 1, (HID,))).astype(np.float32),
+        s_in=signs(seed + 1, HID), s_o=signs(seed + 2, H * D),
+        q=workload.ternary_weights(seed + 3, 2 * H * D, HID), k=workload.ternary_weights(seed + 4, KV * D, HID),
+        v=workload.ternary_weights(seed + 5, KV * D, HID), o=workload.ternary_weights(seed + 6, HID, H * D),
+        qn=(1.0 + 0.1 * oracle.normal(seed, 2, (D,))).astype(np.float32),
+        kn=(1.0 + 0.1 * oracle.normal(seed, 3, (D,))).astype(np.float32),
+        pos=np.stack([p, p, p]), inv=inv_freq(),
+        kc=oracle.f32_to_f16(oracle.rms_rows(oracle.normal(seed, 4, (cap, KV, D)))),
+        vc=oracle.f32_to_f16(oracle.normal(seed, 5, (cap, KV, D))))
+
+
+def oracle_block(b, T, off):
+    xr = oracle.norm_rotate(b["h"], b["in_w"], b["s_in"])
+    qp = oracle.ternary(b["q"][0], b["q"][1], xr).reshape(T, H, 512)
+    kp = oracle.ternary(b["k"][0], b["k"][1], xr).reshape(T, KV, D)
+    vp = oracle.ternary(b["v"][0], b["v"][1], xr).reshape(T, KV, D)
+    kc, vc = b["kc"].copy(), b["vc"].copy()
+    q = oracle.prep(qp, kp, vp, b["qn"], b["kn"], b["pos"], b["inv"], kc, vc, off)
+    attn = oracle.attend(q, kc, vc, off, np.ascontiguousarray(qp[:, :, D:]))
+    qp_inf = np.zeros((T, H, 512), np.float32)
+    qp_inf[:, :, D:] = np.inf  # sigmoid = 1: rotate the already-gated rows
+    xo = oracle.gate_rotate(attn.reshape(T, H * D), qp_inf.reshape(T, -1), b["s_o"])
+    return oracle.ternary(b["o"][0], b["o"][1], xo, y=b["h"]), kc, vc
+
+
+def gpu_block(g, b, T, off):
+    torch, ctx, ws = g
+    d = {k: dev(torch, b[k]) for k in ("h", "in_w", "s_in", "s_o", "qn", "kn", "pos", "inv", "kc", "vc")}
+    mat = lambda m: (dev(torch, m[0]), dev(torch, m[1]))
+    xr = ba.norm_rotate(ctx, d["h"], d["in_w"], d["s_in"])
+    qp = torch.empty((T, H, 512), device="cuda")
+    kp = torch.empty((T, KV, D), device="cuda")
+    vp = torch.empty((T, KV, D), device="cuda")
+    ba.ternary_matmul(ctx, xr, [(*mat(b["q"]), qp.view(T, -1)), (*mat(b["k"]), kp.view(T, -1)),
+                                (*mat(b["v"]), vp.view(T, -1))])
+    xo = ba.attention_layer(ctx, ws, qp, kp, vp, d["qn"], d["kn"], d["pos"], d["inv"], d["kc"], d["vc"], off,
+                            gate=qp[:, :, D:], signs=d["s_o"])
+    ba.ternary_matmul(ctx, xo.view(T, H * D), [(*mat(b["o"]), d["h"])], add=True)
+    torch.cuda.synchronize()
+    return d["h"].cpu().numpy(), d["kc"].cpu().numpy().view(np.uint16), d["vc"].cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("T,off", [(1, 300), (8, 1000), (100, 50)])
+def test_attention_block_matches_oracle_chain(gpu, T, off):
+    print(f"block T={T} off={off}", flush=True)
+    b = block_inputs(0x7400 + T, T, off)
+    h_ref, kc_ref, vc_ref = oracle_block(b, T, off)
+    h_got, kc, vc = gpu_block(gpu, b, T, off)
+    rows = slice(off, off + T)
+    assert_f16_rows_close(kc[rows], kc_ref[rows])
+    assert_f16_rows_close(vc[rows], vc_ref[rows])
+    err = float(np.max(np.abs(h_got - h_ref)))
+    assert err <= 2e-3, err

@@ -406,3 +406,22 @@ def test_ternary_add_and_lora():
     got = oracle.ternary(wz, s, x)
     sf = oracle.f16_to_f32(s).astype(np.float64)
     assert np.max(np.abs(got - (-sf[:, 0][None, :] * x.astype(np.float64).sum(1)[:, None]))) < 1e-4
+
+
+# norm_rotate: float64 closed form (RMS norm, then the Sylvester Hadamard matrix on each 512-block).
+def test_norm_rotate_closed_form():
+    T, Dm = 3, 1536
+    h = oracle.normal(0x7E10, 0, (T, Dm)) * 3.0
+    w = (1.0 + 0.1 * oracle.normal(0x7E10, 1, (Dm,))).astype(np.float32)
+    signs = np.where(oracle.normal(0x7E10, 2, (Dm,)) > 0, 1.0, -1.0).astype(np.float32)
+    xr, xn = oracle.norm_rotate(h, w, signs, want_xn=True)
+    hd = h.astype(np.float64)
+    r = 1.0 / np.sqrt((hd ** 2).mean(1, keepdims=True) + 1e-6)
+    xn_ref = hd * r * w
+    Hm = scipy.linalg.hadamard(512).astype(np.float64)
+    xr_ref = np.concatenate([(xn_ref[:, b:b + 512] * signs[b:b + 512]) @ Hm.T for b in range(0, Dm, 512)], 1)
+    xr_ref /= np.sqrt(512.0)
+    assert np.max(np.abs(xn - xn_ref)) < 1e-5
+    assert np.max(np.abs(xr - xr_ref)) < 2e-5
+    # the rotation is orthogonal: row norms of xr equal those of signs * xn
+    assert np.allclose(np.linalg.norm(xr.astype(np.float64), axis=1), np.linalg.norm(xn_ref, axis=1), rtol=1e-5)
