@@ -272,6 +272,58 @@ class Workloads:
                     tflops=flops / (ms * 1e-3) / 1e12, wall=wall)
 
 
+    def block(self, steps, warmup, T, off, hid=2560, H=16, KV=4, seed=0xB0A5A10B):
+        """One whole attention layer of the 4B model: norm_rotate, the q/k/v projections (one call), bn_attn_layer
+        (prep, attention over the fp16 cache, gate, rotation) and o_proj added into the hidden rows: four library
+        calls, their argument structs built once."""
+        import ctypes
+        torch, ba, ctx = self.torch, self.ba, self.ctx
+        g = self._gen(seed)
+        cap = off + T
+        h = torch.randn(T, hid, device="cuda", generator=g)
+        in_w = 1 + 0.1 * torch.randn(hid, device="cuda", generator=g)
+        s_in, s_o = self.signs(hid // D, seed + 1), self.signs(H, seed + 2)
+
+        def lin(o, k):
+            w = torch.randint(-2 ** 31, 2 ** 31 - 1, (o, k // 16), device="cuda", dtype=torch.int32, generator=g)
+            return w, (0.02 * torch.rand(o, k // 128, device="cuda", generator=g) + 0.005).half().view(torch.int16)
+
+        wq, wk, wv, wo = lin(2 * H * D, hid), lin(KV * D, hid), lin(KV * D, hid), lin(hid, H * D)
+        kc = rms(torch, torch.randn(cap, KV, D, device="cuda", generator=g)).half().view(torch.int16)
+        vc = torch.randn(cap, KV, D, device="cuda", generator=g).half().view(torch.int16)
+        qn = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+        kn = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+        p = torch.arange(off, off + T, device="cuda", dtype=torch.int32)
+        pos = torch.stack([p, p, p]).contiguous()
+        inv = 1.0 / (1e7 ** (torch.arange(32, device="cuda", dtype=torch.float32) * 2 / 64))
+        xr = torch.empty(T, hid, device="cuda")
+        qp = torch.empty(T, H, 512, device="cuda")
+        kp = torch.empty(T, KV, D, device="cuda")
+        vp = torch.empty(T, KV, D, device="cuda")
+        q16 = torch.empty(T, H, D, device="cuda", dtype=torch.float16) if T > ba.VERIFY_MAX else None
+        na = ba.norm_args(h, in_w, s_in, xr)
+        qa = ba.ternary_args(xr, [(*wq, qp.view(T, -1)), (*wk, kp.view(T, -1)), (*wv, vp.view(T, -1))])
+        pa, la, xo = ba.attention_layer_args(ctx, self.ws, qp, kp, vp, qn, kn, pos, inv, kc, vc, off,
+                                             gate=qp[:, :, D:], signs=s_o, q=q16)
+        oa = ba.ternary_args(xo.view(T, H * D), [(*wo, h)], add=True)
+        st, L, by = ctx._stream(None), ctx.lib, ctypes.byref
+
+        def step():
+            ctx._check(L.bn_norm_rotate(ctx.h, st, by(na)), "bn_norm_rotate")
+            ctx._check(L.bn_ternary_matmul(ctx.h, st, by(qa)), "bn_ternary_matmul")
+            ctx._check(L.bn_attn_layer(ctx.h, st, by(pa), by(la)), "bn_attn_layer")
+            ctx._check(L.bn_ternary_matmul(ctx.h, st, by(oa)), "bn_ternary_matmul")
+
+        ms, wall = time_steps(torch, step, steps, warmup)
+        O = 2 * H * D + 2 * KV * D
+        w_bytes = (O * hid + hid * H * D) // 4 + (O * hid + hid * H * D) // 128 * 2
+        # weights (codes, scales) and the cache rows read once; hidden rows read and written
+        nbytes = w_bytes + off * KV * D * 2 * 2 + T * hid * 4 * 3
+        flops = 2 * T * (O * hid + hid * H * D) + attn_flops(H, T, off)
+        return dict(ms=ms, bytes=nbytes, gbs=nbytes / (ms * 1e-3) / 1e9, flops=flops,
+                    tflops=flops / (ms * 1e-3) / 1e12, wall=wall)
+
+
 def measured_traffic(name):
     """HBM bytes per step from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ (its
     `traffic_bytes_per_step:` line), or (None, None) when the summary is absent."""
@@ -325,7 +377,8 @@ def cpu_baseline(budget_s=10.0, H=16, KV=4, L=8192, nseq=2):
 ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix",
        "decode_8k_batch32_rotated", "prefill_4k_rotated", "verify_8_rotated", "prep_4k", "prep_decode",
        "gate_rotate_4k", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k", "kv_copy_8x4k",
-       "qkv_decode_4b", "qkv_verify_8_4b", "qkv_prefill_4k_4b", "o_proj_decode_4b", "o_proj_prefill_4k_4b")
+       "qkv_decode_4b", "qkv_verify_8_4b", "qkv_prefill_4k_4b", "o_proj_decode_4b", "o_proj_prefill_4k_4b",
+       "block_decode_8k_4b", "block_verify_8_4b", "block_prefill_4k_4b")
 # ternary projections of the 4B layer (hidden 2560, 16 q heads, 4 kv heads): q_proj 8192 rows (q and gate halves),
 # k_proj and v_proj 1024 rows each, all over the 2560-wide normed input; o_proj 2560 rows over the 4096-wide
 # rotated attention output, added into the residual
@@ -437,6 +490,13 @@ def main():
             log(name)
             big = cfg["T"] > 16
             res[name] = r = W.ternary(max(2, K // 4) if big else K, max(1, Wm // 2) if big else Wm, **cfg)
+            log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s, {r['tflops']:.1f} TFLOP/s")
+    for name, (T, off) in {"block_decode_8k_4b": (1, 8191), "block_verify_8_4b": (8, 8184),
+                           "block_prefill_4k_4b": (4096, 0)}.items():
+        if name in only:
+            log(name)
+            big = T > 16
+            res[name] = r = W.block(max(2, K // 4) if big else K, max(1, Wm // 2) if big else Wm, T, off)
             log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s, {r['tflops']:.1f} TFLOP/s")
     cpu = None
     if not args.no_cpu_baseline:

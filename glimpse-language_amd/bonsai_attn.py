@@ -422,6 +422,16 @@ def attention_layer(ctx, ws, qp, kp, vp, q_norm, k_norm, pos, inv_freq, kc, vc, 
     """bn_attn_layer: attn_prep + attention (+ gate, + rotation with signs) in one call. qp [T, H, >=256] raw q
     rows (q_proj's output as it is), kp/vp [T, KV, 256] raw; gate a [T, H, 256] view with unit stride in the
     last dim (e.g. qp[:, :, 256:]); q: scratch [T, H, 256] for T > 16 (allocated when None)."""
+    p, a, out = attention_layer_args(ctx, ws, qp, kp, vp, q_norm, k_norm, pos, inv_freq, kc, vc, off, gate, signs,
+                                     out, q, rot, s1, s2)
+    st = ctx.lib.bn_attn_layer(ctx.h, ctx._stream(stream), ctypes.byref(p), ctypes.byref(a))
+    ctx._check(st, "bn_attn_layer")
+    return out
+
+
+def attention_layer_args(ctx, ws, qp, kp, vp, q_norm, k_norm, pos, inv_freq, kc, vc, off, gate=None, signs=None,
+                         out=None, q=None, rot=64, s1=11, s2=11):
+    """The (bn_prep_args, bn_attn_args, out) of an attention_layer call, for callers that issue it repeatedly."""
     import torch
     T, H = qp.shape[0], qp.shape[1]
     KV, cap = kc.shape[1], kc.shape[0]
@@ -448,9 +458,7 @@ def attention_layer(ctx, ws, qp, kp, vp, q_norm, k_norm, pos, inv_freq, kc, vc, 
     buf = ws.get(need) if ws is not None else None
     a.ws = _ptr(buf)
     a.ws_bytes = 0 if buf is None else buf.numel()
-    st = ctx.lib.bn_attn_layer(ctx.h, ctx._stream(stream), ctypes.byref(p), ctypes.byref(a))
-    ctx._check(st, "bn_attn_layer")
-    return out
+    return p, a, out
 
 
 def kv_state(kc, vc, length):

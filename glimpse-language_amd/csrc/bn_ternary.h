@@ -221,6 +221,16 @@ __device__ __forceinline__ void tern_sync() {
     }
 }
 
+// LDS row of token row m in block k = 2q + kg of a staged chunk: m XOR a per-block mask, a bijection inside each
+// 16-row group. Staging writes 8 (or 16) consecutive lanes to the same m in consecutive blocks, which start BM * 16
+// bytes apart (the same banks); the mask spreads them over distinct 16-byte bank slots, and the A-operand reads
+// (32 consecutive m per block) stay a permutation of slots within every 8- and 16-lane group.
+template <int NQ>
+__device__ __forceinline__ int tern_swz(int m, int k) {
+    if constexpr (NQ == 4) return m ^ (k | ((m & 1) << 3));
+    else return m ^ (k & 15);
+}
+
 // MT 32-token tiles x 2 32-row tiles per wave; KS waves split K (their partial sums meet in LDS in ks order), RG
 // waves split rows (KS > 1 only with RG = 1). Block: 64 * KS * RG threads, 32 * MT tokens x 64 * RG rows.
 //
@@ -286,7 +296,7 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
                 lo[2 * s] = (_Float16)(xa[i][s] - (float)hi[2 * s]);
                 lo[2 * s + 1] = (_Float16)(xb[i][s] - (float)hi[2 * s + 1]);
             }
-            const int off = ((q * 2 + kgu) * BM + mm) * 8;
+            const int off = ((q * 2 + kgu) * BM + tern_swz<NQ>(mm, q * 2 + kgu)) * 8;
             *reinterpret_cast<h8*>(glds + off) = hi;
             *reinterpret_cast<h8*>(glds + 2 * NQ * BM * 8 + off) = lo;
         }
@@ -303,11 +313,14 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
         srow[nt] = m.s + row * kg;
     }
     u4 wv[2][NQ / 4];
+    uint16_t sv_next[2] = {0, 0};  // the next chunk's scales, loaded with its codes
     auto load_w = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
             for (int h = 0; h < NQ / 4; ++h) wv[nt][h] = *reinterpret_cast<const u4*>(wrow[nt] + c * (KC / 16) + 4 * h);
+            sv_next[nt] = srow[nt][(kbase + c * KC) >> 7];
+        }
     };
 
     f16x acc[MT][2];
@@ -319,10 +332,10 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
             for (int e = 0; e < 16; ++e) acc[i][nt][e] = 0.0f;
 
     const int shift = kgl ? 0 : 8;
-    auto scales = [&](int c, h2 (&s2)[2]) __attribute__((always_inline)) {
+    auto scales = [&](h2 (&s2)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-            const _Float16 sv = active ? __builtin_bit_cast(_Float16, srow[nt][(kbase + c * KC) >> 7]) : (_Float16)0;
+            const _Float16 sv = __builtin_bit_cast(_Float16, sv_next[nt]);
             s2[nt] = h2{sv, sv};
         }
     };
@@ -338,7 +351,7 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
             wcur[1][h] = wv[1][h];
         }
         h2 s2[2];
-        scales(c, s2);
+        scales(s2);
         tern_sync<KS>();
         if (c + 1 < nchunk) {
             load_x(c + 1);
@@ -353,7 +366,7 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
                 h8 ah[MT], al[MT];
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
-                    const int off = ((q * 2 + kgl) * BM + 32 * i + n) * 8;
+                    const int off = ((q * 2 + kgl) * BM + tern_swz<NQ>(32 * i + n, q * 2 + kgl)) * 8;
                     ah[i] = *reinterpret_cast<const h8*>(glds + off);
                     al[i] = *reinterpret_cast<const h8*>(glds + 2 * NQ * BM * 8 + off);
                 }
