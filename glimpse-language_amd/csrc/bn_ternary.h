@@ -191,16 +191,19 @@ constexpr int TERN_KC = 64;  // k per staged chunk (4 MFMA k-steps of 16)
 #define BN_TERN_PF_KC 64
 #endif
 
-// 8 codes of word `wd` as fp16 (code - 1) * s: slots 2i, 2i+1 = codes 4kg + i, 12... see the A layout below.
-// wd2 = kg ? wd : wd << 8 puts the lane's codes (4kg + i, 8 + 4kg + i) at bits [8 + 2i, ..) and [24 + 2i, ..).
+// 8 codes of a word as fp16 (code - 1) * s: slots 2i, 2i+1 = codes 4kg + i, 8 + 4kg + i (the A layout below).
+// wd2 = (word ^ 0x55555555) << (kg ? 0 : 8): every code is flipped to code ^ 1, and the lane's codes land at bits
+// [8 + 2i, ..) and [24 + 2i, ..).
 __device__ __forceinline__ h8 tern_decode8(uint32_t wd2, h2 s2) {
     h8 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        // selector bytes 1 and 3 = the two codes (0..3, table bytes), bytes 0 and 2 = 0x0C (zero byte)
-        const uint32_t sel = ((wd2 >> (2 * i)) & 0x03000300u) | 0x000C000Cu;
-        // table: byte c = high byte of fp16(c - 1): -1 0xBC00, 0 0x0000, 1 0x3C00, 2 0x4000
-        const uint32_t hv = __builtin_amdgcn_perm(0u, 0x403C00BCu, sel);
+        // selector bytes 1 and 3 = the two flipped codes (table bytes 0..3), bytes 0 and 2 = 0 (table byte 0, the
+        // zero high byte of code 1, which is also the low byte of every fp16 result)
+        const uint32_t sel = (wd2 >> (2 * i)) & 0x03000300u;
+        // table byte (code ^ 1) = high byte of fp16(code - 1): code 1 -> 0x00, 0 -> 0xBC (-1), 3 -> 0x40 (2),
+        // 2 -> 0x3C (1)
+        const uint32_t hv = __builtin_amdgcn_perm(0u, 0x3C40BC00u, sel);
         const h2 v = __builtin_bit_cast(h2, hv) * s2;  // exact: (code - 1) * s is -s, 0, s or 2s
         r[2 * i] = v[0];
         r[2 * i + 1] = v[1];
@@ -288,13 +291,17 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
             const int u = gt + i * GT;
             const int mm = u / (2 * NQ), q = (u >> 1) % NQ, kgu = u & 1;
             if (t0 + mm >= a.T) continue;
+            // hi = x with its low 13 mantissa bits cleared (exact in fp16 for fp16-range x), lo = x - hi (exact in
+            // fp32), rounded to fp16: hi + lo carries 22 of x's 24 significant bits
             h8 hi, lo;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                hi[2 * s] = (_Float16)xa[i][s];
-                hi[2 * s + 1] = (_Float16)xb[i][s];
-                lo[2 * s] = (_Float16)(xa[i][s] - (float)hi[2 * s]);
-                lo[2 * s + 1] = (_Float16)(xb[i][s] - (float)hi[2 * s + 1]);
+                const float ha = __uint_as_float(__float_as_uint(xa[i][s]) & 0xFFFFE000u);
+                const float hb = __uint_as_float(__float_as_uint(xb[i][s]) & 0xFFFFE000u);
+                hi[2 * s] = (_Float16)ha;
+                hi[2 * s + 1] = (_Float16)hb;
+                lo[2 * s] = (_Float16)(xa[i][s] - ha);
+                lo[2 * s + 1] = (_Float16)(xb[i][s] - hb);
             }
             const int off = ((q * 2 + kgu) * BM + tern_swz<NQ>(mm, q * 2 + kgu)) * 8;
             *reinterpret_cast<h8*>(glds + off) = hi;
@@ -362,7 +369,7 @@ __global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row
             for (int q = 0; q < NQ; ++q) {
                 h8 b[2];
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) b[nt] = tern_decode8(wcur[nt][q >> 2][q & 3] << shift, s2[nt]);
+                for (int nt = 0; nt < 2; ++nt) b[nt] = tern_decode8((wcur[nt][q >> 2][q & 3] ^ 0x55555555u) << shift, s2[nt]);
                 h8 ah[MT], al[MT];
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
