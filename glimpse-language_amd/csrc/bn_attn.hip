@@ -586,6 +586,11 @@ bn_status check_norm(const bn_norm_args* a, char* why) {
     return BN_OK;
 }
 
+// tokens up to which the VALU rows kernel runs (4 or 8); more take the MFMA kernels
+#ifndef BN_TERN_ROWS_MAX_T
+#define BN_TERN_ROWS_MAX_T 4
+#endif
+
 // K split of the small-T MFMA kernel: 4 ways when each quarter of K is whole 64-column chunks, else 2 (k is a
 // multiple of 128)
 int tern_ksplit(uint32_t k) { return (k % (4 * bn::TERN_KC) == 0) ? 4 : 2; }
@@ -613,13 +618,19 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
     t.lu = a->lora_u;
     t.lu_ts = a->lora_us;
     t.lr = (int)a->lora_r;
-    if (a->T <= 4) {
+    if (a->T <= BN_TERN_ROWS_MAX_T) {
         const dim3 grid((unsigned)ceil_div(rows, 4 * bn::TERN_ROWS_WAVE));
         switch (a->T) {
             case 1: hipLaunchKernelGGL(bn::tern_rows_kernel<1>, grid, dim3(256), 0, st, t); break;
             case 2: hipLaunchKernelGGL(bn::tern_rows_kernel<2>, grid, dim3(256), 0, st, t); break;
             case 3: hipLaunchKernelGGL(bn::tern_rows_kernel<3>, grid, dim3(256), 0, st, t); break;
-            default: hipLaunchKernelGGL(bn::tern_rows_kernel<4>, grid, dim3(256), 0, st, t); break;
+            case 4: hipLaunchKernelGGL(bn::tern_rows_kernel<4>, grid, dim3(256), 0, st, t); break;
+#if BN_TERN_ROWS_MAX_T > 4
+            case 5: hipLaunchKernelGGL(bn::tern_rows_kernel<5>, grid, dim3(256), 0, st, t); break;
+            case 6: hipLaunchKernelGGL(bn::tern_rows_kernel<6>, grid, dim3(256), 0, st, t); break;
+            case 7: hipLaunchKernelGGL(bn::tern_rows_kernel<7>, grid, dim3(256), 0, st, t); break;
+            default: hipLaunchKernelGGL(bn::tern_rows_kernel<8>, grid, dim3(256), 0, st, t); break;
+#endif
         }
         return launched(ctx, "tern_rows_kernel");
     }
@@ -627,7 +638,10 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
         // one 32-token tile, 64 rows per block, K split over the block's waves
         const int row_tiles = (int)(rows / 64);
         const dim3 grid((unsigned)row_tiles);
-        if (tern_ksplit(a->k) == 4)
+        // fewer 64-row tiles than CUs (o_proj-sized matrices): 8 waves per block split K further
+        if (row_tiles < ctx->cus && a->k % (8 * bn::TERN_KC) == 0)
+            hipLaunchKernelGGL((bn::tern_mfma_kernel<1, 8, 1>), grid, dim3(512), 0, st, t, row_tiles);
+        else if (tern_ksplit(a->k) == 4)
             hipLaunchKernelGGL((bn::tern_mfma_kernel<1, 4, 1>), grid, dim3(256), 0, st, t, row_tiles);
         else
             hipLaunchKernelGGL((bn::tern_mfma_kernel<1, 2, 1>), grid, dim3(128), 0, st, t, row_tiles);

@@ -241,10 +241,10 @@ __device__ __forceinline__ int tern_swz(int m, int k) {
 // holds x[m][k0 + 16q + 4kg + 8(i & 1) + (i >> 1)], the k order tern_decode8 gives the B operand, so each lane's A
 // operand (m = lane % 32, kg = lane / 32) is one 16-byte LDS read.
 template <int MT, int KS, int RG, int OCC = 1, int KC = TERN_KC>
-__global__ __launch_bounds__(256, OCC) void tern_mfma_kernel(TernArgs a, int row_tiles) {
+__global__ __launch_bounds__(64 * KS * RG, OCC) void tern_mfma_kernel(TernArgs a, int row_tiles) {
     constexpr int NQ = KC / 16;        // MFMA k-steps per chunk
     static_assert(KC == 64 || KC == 128, "a chunk lies inside one 128-column scale group");
-    static_assert(KS * RG <= 4 && (KS == 1 || (RG == 1 && MT == 1)), "split-K blocks are one token tile, one row group");
+    static_assert(KS * RG <= 8 && (KS == 1 || (RG == 1 && MT == 1)), "split-K blocks are one token tile, one row group");
     constexpr int BM = 32 * MT;        // tokens per block
     constexpr int GROUP_H = 2 * NQ * 2 * BM * 8;  // fp16 per k-split group (hi and lo): NQ q * 2 kg * BM * 8 * 2
     // one buffer, two syncs per chunk: a second buffer costs registers and occupancy (3 -> 2 waves per SIMD for

@@ -3,7 +3,7 @@
 Every output is within workload.ternary_tolerance of the oracle: 2e-5 of the L2 norm of its K products (fp32 sums in
 another order differ by about 3e-6 of it; a path that rounded x to fp16 would be off by about 2.4e-4), and within the
 north-star max-abs 2e-3. Repeated calls are bit-identical. Cases cover each kernel: the VALU rows kernel (T = 1..4),
-the split-K MFMA kernel (T = 5..32, K split 4 or 2 ways), the 128-token MFMA kernel (T > 32, partly empty token
+the split-K MFMA kernel (T = 5..32, K split 8, 4 or 2 ways), the 128-token MFMA kernel (T > 32, partly empty token
 and row tiles), one to three matrices sharing x, add into y, LoRA, code 3 and strided rows.
 """
 import numpy as np
@@ -64,7 +64,8 @@ CASES = [
     (1, 2048, (4096, 512, 512)),   # 2B q/k/v decode step
     (1, 2560, (2560,)),            # 4B o_proj-sized decode
     (2, 2048, (512,)), (3, 384, (64, 128)), (4, 1024, (192,)),
-    (5, 2048, (256,)), (8, 2560, (8192, 1024, 1024)),   # 4B verify rows: K split 4 ways
+    (5, 2048, (256,)), (8, 2560, (8192, 1024, 1024)),   # 4B verify rows: K split 8 ways (fewer tiles than CUs)
+    (6, 768, (128,)),              # K split 4 ways (768 = 4 * 192)
     (16, 384, (64, 64, 64)),       # K split 2 ways (384 = 2 * 192)
     (12, 640, (128,)),             # K split 2 ways (640 = 2 * 320, scale groups straddle the halves)
     (32, 2048, (512,)), (33, 256, (704,)),              # first 128-token tile: partly empty token and row tiles
