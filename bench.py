@@ -65,7 +65,8 @@ def rms(torch, x):
 def time_steps(torch, fn, steps, warmup):
     """Runs `warmup` untimed steps, then `steps` timed ones bracketed by synchronisations. Two HIP events recorded
     on the launch stream (torch's current stream, where the library launches) around the timed steps give the
-    average step duration; a step is one library call."""
+    average step duration; a step is one library call with its argument structs built beforehand (as a compiled
+    caller holds them), so host-side Python does not pace the small calls."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -115,9 +116,9 @@ class Workloads:
         max_len = max(lens)
         signs = self.signs(H) if rotate else None
 
-        def step():
-            ba.decode_ragged(ctx, self.ws, q, kc, vc, kv_off, kv_len, max_len, out=out, k_new=k_new, v_new=v_new,
-                             gate=gate, signs=signs)
+        a, _ = ba.decode_ragged_args(ctx, self.ws, q, kc, vc, kv_off, kv_len, max_len, out=out, k_new=k_new,
+                                     v_new=v_new, gate=gate, signs=signs)
+        step = ba.bind(ctx, "bn_attn_decode_ragged", a)
 
         ms, wall = time_steps(torch, step, steps, warmup)
         nbytes = decode_bytes(H, KV, lens)
@@ -139,9 +140,9 @@ class Workloads:
         out = torch.empty(T, H, D, device="cuda")
         signs = self.signs(H) if rotate else None
 
-        def step():
-            ba.attention(ctx, self.ws, q, kc, vc, off, out=out, k_new=k_new, v_new=v_new, gate=gate, kind=kind,
-                         signs=signs)
+        a, _ = ba.attention_args(ctx, self.ws, q, kc, vc, off, out=out, k_new=k_new, v_new=v_new, gate=gate,
+                                 signs=signs)
+        step = ba.bind(ctx, ba._KIND_FN[kind], a)
 
         ms, wall = time_steps(torch, step, steps, warmup)
         flops = attn_flops(H, T, off)
@@ -167,8 +168,7 @@ class Workloads:
         vc = torch.empty_like(kc)
         q = torch.empty(T, H, D, device="cuda")
 
-        def step():
-            ba.attn_prep(ctx, qp, kp, vp, qn, kn, pos, inv, kc, vc, off, q=q)
+        step = ba.bind(ctx, "bn_attn_prep", ba.prep_args(qp, kp, vp, qn, kn, pos, inv, q, kc, vc, off))
 
         ms, wall = time_steps(torch, step, steps, warmup)
         nbytes = T * H * D * 4 * 2 + T * KV * D * 4 * 2 + T * KV * D * 2 * 2 + 3 * T * 4
@@ -183,8 +183,7 @@ class Workloads:
         signs = self.signs(H)
         xr = torch.empty(T, H * D, device="cuda")
 
-        def step():
-            ba.gate_rotate(ctx, attn, signs, gate=qp[:, :, D:], xr=xr)
+        step = ba.bind(ctx, "bn_gate_rotate", ba.rotate_args(attn, signs, xr, qp[:, :, D:]))
 
         ms, wall = time_steps(torch, step, steps, warmup)
         nbytes = 3 * T * H * D * 4 + H * D * 4
@@ -212,9 +211,9 @@ class Workloads:
         # a prefill's q goes through an fp16 scratch (BN_Q_F16), the form prefill_kernel reads fastest
         q = torch.empty(T, H, D, device="cuda", dtype=torch.float16) if T > ba.VERIFY_MAX else None
 
-        def step():
-            ba.attention_layer(ctx, self.ws, qp, kp, vp, qn, kn, pos, inv, kc, vc, off, gate=qp[:, :, D:],
-                               signs=signs, out=out, q=q)
+        pa, la, _ = ba.attention_layer_args(ctx, self.ws, qp, kp, vp, qn, kn, pos, inv, kc, vc, off, gate=qp[:, :, D:],
+                                            signs=signs, out=out, q=q)
+        step = ba.bind(ctx, "bn_attn_layer", pa, la)
 
         ms, wall = time_steps(torch, step, steps, warmup)
         flops = attn_flops(H, T, off)
@@ -235,8 +234,7 @@ class Workloads:
         sv = torch.empty_like(sk)
         src, dst = ba.kv_state(kc, vc, length), ba.kv_state(sk, sv, 0)
 
-        def step():
-            ba.kv_copy(ctx, src, dst)
+        step = ba.bind(ctx, "bn_kv_copy", src, dst)
 
         ms, wall = time_steps(torch, step, steps, warmup)
         nbytes = 2 * 2 * n_layers * length * KV * D * 2  # K and V, read and written
@@ -254,14 +252,7 @@ class Workloads:
             sc = (0.02 * torch.rand(o, K // 128, device="cuda", generator=g) + 0.005).half().view(torch.int16)
             mats.append((w, sc, torch.zeros(T, o, device="cuda")))
 
-        # the argument struct is built once: a step is the library call alone (its launch is a few microseconds,
-        # below what building the ctypes struct in Python costs)
-        import ctypes
-        args = ba.ternary_args(x, mats, add)
-        stream = ctx._stream(None)
-
-        def step():
-            ctx._check(ctx.lib.bn_ternary_matmul(ctx.h, stream, ctypes.byref(args)), "bn_ternary_matmul")
+        step = ba.bind(ctx, "bn_ternary_matmul", ba.ternary_args(x, mats, add))
 
         ms, wall = time_steps(torch, step, steps, warmup)
         O = sum(os)

@@ -324,6 +324,19 @@ _KIND_FN = {KIND_FORWARD: "bn_attn_forward", KIND_DECODE: "bn_attn_decode", KIND
             KIND_PREFILL: "bn_attn_prefill", KIND_APPEND: "bn_attn_append"}
 
 
+def bind(ctx, name, *structs, stream=None):
+    """A zero-argument callable that issues library entry `name` on `stream` with argument structs built once
+    (as a compiled caller would), checking the status."""
+    f = getattr(ctx.lib, name)
+    st = ctx._stream(stream)
+    refs = [ctypes.byref(x) for x in structs]
+
+    def call():
+        ctx._check(f(ctx.h, st, *refs), name)
+    call.structs = structs
+    return call
+
+
 def attention(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=None, kind=KIND_FORWARD,
               stream=None, q_strides=None, g_strides=None, signs=None):
     """One attention-layer call: append k_new/v_new at [off, off+T), attend causally, gate (and, with signs,
@@ -332,6 +345,14 @@ def attention(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=No
     q: [T, H, 256] fp32, or fp16 (passed with BN_Q_F16); kc/vc: [cap, KV, 256] fp16 (torch.float16 or int16
     view); out: [T, H, 256] fp32; signs: [H * 256] fp32 +-1.
     """
+    a, out = attention_args(ctx, ws, q, kc, vc, off, out, k_new, v_new, gate, q_strides, g_strides, signs)
+    ctx.call(_KIND_FN[kind], a, stream)
+    return out
+
+
+def attention_args(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=None, q_strides=None,
+                   g_strides=None, signs=None):
+    """The bn_attn_args of an attention() call (workspace attached) and its output tensor."""
     import torch
     T, H = q.shape[0], q.shape[1]
     cap, KV = kc.shape[0], kc.shape[1]
@@ -344,12 +365,19 @@ def attention(ctx, ws, q, kc, vc, off, out=None, k_new=None, v_new=None, gate=No
     buf = ws.get(need) if ws is not None else None
     a.ws = _ptr(buf)
     a.ws_bytes = 0 if buf is None else buf.numel()
-    ctx.call(_KIND_FN[kind], a, stream)
-    return out
+    return a, out
 
 
 def decode_ragged(ctx, ws, q, kc, vc, kv_off, kv_len, max_len, out=None, k_new=None, v_new=None, gate=None,
                   stream=None, signs=None):
+    a, out = decode_ragged_args(ctx, ws, q, kc, vc, kv_off, kv_len, max_len, out, k_new, v_new, gate, signs)
+    ctx.call("bn_attn_decode_ragged", a, stream)
+    return out
+
+
+def decode_ragged_args(ctx, ws, q, kc, vc, kv_off, kv_len, max_len, out=None, k_new=None, v_new=None, gate=None,
+                       signs=None):
+    """The bn_ragged_args of a decode_ragged() call (workspace attached) and its output tensor."""
     import torch
     nseq, H = q.shape[0], q.shape[1]
     KV = kc.shape[1]
@@ -360,8 +388,7 @@ def decode_ragged(ctx, ws, q, kc, vc, kv_off, kv_len, max_len, out=None, k_new=N
     buf = ws.get(need) if ws is not None else None
     a.ws = _ptr(buf)
     a.ws_bytes = 0 if buf is None else buf.numel()
-    ctx.call("bn_attn_decode_ragged", a, stream)
-    return out
+    return a, out
 
 
 def prep_args(qp, kp, vp, q_norm, k_norm, pos, inv_freq, q, kc, vc, off, rot=64, s1=11, s2=11):
