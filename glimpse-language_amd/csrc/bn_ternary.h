@@ -277,9 +277,12 @@ __global__ __launch_bounds__(64 * KS * RG, OCC) void tern_mfma_kernel(TernArgs a
         for (int i = 0; i < UPT; ++i) {
             const int u = gt + i * GT;
             const int mm = u / (2 * NQ), q = (u >> 1) % NQ, kgu = u & 1;
-            // token rows past T are neither loaded nor staged: their A rows only feed outputs that are not stored
-            if (t0 + mm < a.T) {
-                const float* p = a.x + (int64_t)(t0 + mm) * a.x_ts + kbase + c * KC + 16 * q + 4 * kgu;
+            // token rows past T are not staged: their A rows only feed outputs that are not stored. Prefill blocks
+            // (KS = 1) load them anyway from row T - 1 (in bounds), so that the next chunk's loads are unconditional
+            // and stay in flight (a conditional load leaves register copies that the compiler waits for right after
+            // issuing the next loads); split-K blocks of a few tokens skip them.
+            if (KS == 1 || t0 + mm < a.T) {
+                const float* p = a.x + (int64_t)min(t0 + mm, a.T - 1) * a.x_ts + kbase + c * KC + 16 * q + 4 * kgu;
                 xa[i] = *reinterpret_cast<const f4*>(p);
                 xb[i] = *reinterpret_cast<const f4*>(p + 8);
             }
@@ -346,8 +349,9 @@ __global__ __launch_bounds__(64 * KS * RG, OCC) void tern_mfma_kernel(TernArgs a
             s2[nt] = h2{sv, sv};
         }
     };
+    // inactive waves (rows past the last matrix) load member 0's first rows, in bounds, and do not use them
     load_x(0);
-    if (active) load_w(0);
+    load_w(0);
     for (int c = 0; c < nchunk; ++c) {
         tern_sync<KS>();  // the previous chunk's A reads are done
         store_x();
@@ -356,13 +360,19 @@ __global__ __launch_bounds__(64 * KS * RG, OCC) void tern_mfma_kernel(TernArgs a
         for (int h = 0; h < NQ / 4; ++h) {
             wcur[0][h] = wv[0][h];
             wcur[1][h] = wv[1][h];
+            // the copy happens here, before the next chunk's loads are issued (its wait then covers only the loads
+            // of this chunk, which had the previous chunk's compute to land)
+            asm volatile("" ::"v"(wcur[0][h][0]), "v"(wcur[0][h][1]), "v"(wcur[0][h][2]), "v"(wcur[0][h][3]),
+                         "v"(wcur[1][h][0]), "v"(wcur[1][h][1]), "v"(wcur[1][h][2]), "v"(wcur[1][h][3]));
         }
         h2 s2[2];
         scales(s2);
+        asm volatile("" ::"v"(s2[0]), "v"(s2[1]));
         tern_sync<KS>();
-        if (c + 1 < nchunk) {
-            load_x(c + 1);
-            if (active) load_w(c + 1);
+        if (KS == 1 || c + 1 < nchunk) {
+            const int cn = min(c + 1, nchunk - 1);  // prefill blocks: the last chunk reloads itself (unused)
+            load_x(cn);
+            load_w(cn);
         }
         if (active) {
 #pragma unroll
