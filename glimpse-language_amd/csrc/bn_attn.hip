@@ -964,6 +964,10 @@ bn_status bn_norm_rotate(bn_ctx* ctx, bn_stream stream, const bn_norm_args* a) {
     n.xr_ts = a->xr_ts;
     n.T = (int)a->T;
     n.D = (int)a->d;
+    if (a->d <= 16 * 512) {
+        hipLaunchKernelGGL(bn::norm_rotate_row_kernel, dim3(a->T), dim3(64 * (a->d / 512)), 0, (hipStream_t)stream, n);
+        return launched(ctx, "norm_rotate_row_kernel");
+    }
     hipLaunchKernelGGL(bn::norm_rotate_kernel, dim3(a->T, a->d / 512), dim3(64), 0, (hipStream_t)stream, n);
     return launched(ctx, "norm_rotate_kernel");
 }

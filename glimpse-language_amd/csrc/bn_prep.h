@@ -232,4 +232,45 @@ __global__ __launch_bounds__(64) void norm_rotate_kernel(NormRotateArgs a) {
             f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512;
 }
 
+// norm_rotate with one block per row, D / 512 <= 16 waves: each wave squares and sums its own 512 elements, the
+// partial sums meet in LDS (wave order), so the row is read once (norm_rotate_kernel reads it D / 512 times).
+__global__ __launch_bounds__(1024) void norm_rotate_row_kernel(NormRotateArgs a) {
+    __shared__ float ss_lds[16];
+    const int t = blockIdx.x, lane = threadIdx.x & 63, b = threadIdx.x >> 6, nb = a.D / 512;
+    const float* x = a.h + t * a.h_ts;
+    f4 xv[2], wv[2], sv[2];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int e = 512 * b + 256 * i + 4 * lane;
+        xv[i] = *reinterpret_cast<const f4*>(x + e);
+        wv[i] = *reinterpret_cast<const f4*>(a.w + e);
+        sv[i] = *reinterpret_cast<const f4*>(a.signs + e);
+#pragma unroll
+        for (int c = 0; c < 4; c++) ss = fmaf(xv[i][c], xv[i][c], ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) ss_lds[b] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int k = 0; k < nb; k++) tot += ss_lds[k];
+    const float r = 1.0f / sqrtf(tot / (float)a.D + 1e-6f);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        f4 n;
+#pragma unroll
+        for (int c = 0; c < 4; c++) n[c] = (xv[i][c] * r) * wv[i][c];
+        if (a.xn) *reinterpret_cast<f4*>(a.xn + t * a.xn_ts + 512 * b + 256 * i + 4 * lane) = n;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[4 * i + c] = n[c] * sv[i][c];
+    }
+    fwht512_wave(v, lane);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        *reinterpret_cast<f4*>(a.xr + t * a.xr_ts + 512 * b + 256 * i + 4 * lane) =
+            f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512;
+}
+
 }  // namespace bn

@@ -43,7 +43,7 @@ def dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-@pytest.mark.parametrize("T,Dm", [(1, 512), (5, 2048), (300, 2560)])
+@pytest.mark.parametrize("T,Dm", [(1, 512), (5, 2048), (300, 2560), (2, 8704)])  # 8704: the wave-per-block kernel (d > 8192)
 def test_norm_rotate_matches_oracle(gpu, T, Dm):
     torch, ctx, _ = gpu
     h = oracle.normal(0x7300 + T, 0, (T, Dm)) * np.float32(2.0)
