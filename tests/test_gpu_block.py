@@ -16,6 +16,7 @@ from glimpse_language_amd import bonsai_attn as ba
 pytestmark = pytest.mark.gpu
 D = 256
 HID, H, KV = 2048, 8, 2
+SHAPES = {"2b": (2048, 8, 2), "4b": (2560, 16, 4)}  # hidden, query heads, kv heads
 
 
 def assert_f16_rows_close(got, ref):
@@ -57,7 +58,7 @@ def test_norm_rotate_matches_oracle(gpu, T, Dm):
     assert np.max(np.abs(xr.cpu().numpy() - ref_xr)) <= 2e-5
 
 
-def block_inputs(seed, T, off):
+def block_inputs(seed, T, off, HID=HID, H=H, KV=KV):
     cap = off + T
     p = np.arange(off, off + T, dtype=np.int32)
     return dict(
@@ -73,7 +74,7 @@ def block_inputs(seed, T, off):
         vc=oracle.f32_to_f16(oracle.normal(seed, 5, (cap, KV, D))))
 
 
-def oracle_block(b, T, off):
+def oracle_block(b, T, off, H=H, KV=KV):
     xr = oracle.norm_rotate(b["h"], b["in_w"], b["s_in"])
     qp = oracle.ternary(b["q"][0], b["q"][1], xr).reshape(T, H, 512)
     kp = oracle.ternary(b["k"][0], b["k"][1], xr).reshape(T, KV, D)
@@ -87,7 +88,7 @@ def oracle_block(b, T, off):
     return oracle.ternary(b["o"][0], b["o"][1], xo, y=b["h"]), kc, vc
 
 
-def gpu_block(g, b, T, off):
+def gpu_block(g, b, T, off, H=H, KV=KV):
     torch, ctx, ws = g
     d = {k: dev(torch, b[k]) for k in ("h", "in_w", "s_in", "s_o", "qn", "kn", "pos", "inv", "kc", "vc")}
     mat = lambda m: (dev(torch, m[0]), dev(torch, m[1]))
@@ -104,12 +105,13 @@ def gpu_block(g, b, T, off):
     return d["h"].cpu().numpy(), d["kc"].cpu().numpy().view(np.uint16), d["vc"].cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("T,off", [(1, 300), (8, 1000), (100, 50)])
-def test_attention_block_matches_oracle_chain(gpu, T, off):
-    print(f"block T={T} off={off}", flush=True)
-    b = block_inputs(0x7400 + T, T, off)
-    h_ref, kc_ref, vc_ref = oracle_block(b, T, off)
-    h_got, kc, vc = gpu_block(gpu, b, T, off)
+@pytest.mark.parametrize("T,off,shape", [(1, 300, "2b"), (8, 1000, "2b"), (100, 50, "2b"), (1, 777, "4b"), (40, 90, "4b")])
+def test_attention_block_matches_oracle_chain(gpu, T, off, shape):
+    hid, nh, nkv = SHAPES[shape]
+    print(f"block T={T} off={off} shape={shape}", flush=True)
+    b = block_inputs(0x7400 + T, T, off, hid, nh, nkv)
+    h_ref, kc_ref, vc_ref = oracle_block(b, T, off, nh, nkv)
+    h_got, kc, vc = gpu_block(gpu, b, T, off, nh, nkv)
     rows = slice(off, off + T)
     assert_f16_rows_close(kc[rows], kc_ref[rows])
     assert_f16_rows_close(vc[rows], vc_ref[rows])

@@ -70,6 +70,7 @@ CASES = [
     (12, 640, (128,)),             # K split 2 ways (640 = 2 * 320, scale groups straddle the halves)
     (32, 2048, (512,)), (33, 256, (704,)),              # first 128-token tile: partly empty token and row tiles
     (130, 2048, (512, 128, 128)), (300, 1024, (320,)),
+    (1, 128, (64,)), (8, 128, (64,)), (40, 128, (128,)),   # K = 128: one scale group, one or two chunks
 ]
 
 
