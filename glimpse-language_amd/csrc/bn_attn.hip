@@ -591,6 +591,11 @@ bn_status check_norm(const bn_norm_args* a, char* why) {
 #define BN_TERN_ROWS_MAX_T 4
 #endif
 
+// one-token calls with at least this many columns split each row group's words over two waves
+#ifndef BN_TERN_ROWS_SPLIT_K
+#define BN_TERN_ROWS_SPLIT_K 2048
+#endif
+
 // K split of the small-T MFMA kernel: 4 ways when each quarter of K is whole 64-column chunks, else 2 (k is a
 // multiple of 128)
 int tern_ksplit(uint32_t k) { return (k % (4 * bn::TERN_KC) == 0) ? 4 : 2; }
@@ -621,7 +626,14 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
     if (a->T <= BN_TERN_ROWS_MAX_T) {
         const dim3 grid((unsigned)ceil_div(rows, 4 * bn::TERN_ROWS_WAVE));
         switch (a->T) {
-            case 1: hipLaunchKernelGGL(bn::tern_rows_kernel<1>, grid, dim3(256), 0, st, t); break;
+            case 1:
+                // long rows: two waves split each row group's words (half the serial passes per wave)
+                if (a->k >= BN_TERN_ROWS_SPLIT_K)
+                    hipLaunchKernelGGL((bn::tern_rows_kernel<1, 2>), dim3((unsigned)ceil_div(rows, 2 * bn::TERN_ROWS_WAVE)),
+                                       dim3(256), 0, st, t);
+                else
+                    hipLaunchKernelGGL(bn::tern_rows_kernel<1>, grid, dim3(256), 0, st, t);
+                break;
             case 2: hipLaunchKernelGGL(bn::tern_rows_kernel<2>, grid, dim3(256), 0, st, t); break;
             case 3: hipLaunchKernelGGL(bn::tern_rows_kernel<3>, grid, dim3(256), 0, st, t); break;
             case 4: hipLaunchKernelGGL(bn::tern_rows_kernel<4>, grid, dim3(256), 0, st, t); break;

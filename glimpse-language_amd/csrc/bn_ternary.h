@@ -95,13 +95,17 @@ __device__ __forceinline__ float wave_sum4(const float (&v)[4], int lane) {
 
 // T = NT <= 4 tokens. Each wave: 4 rows of one member; lane l takes words j = l, l + 64, ..., the next word's
 // codes, scales and x loaded while the current one is summed.
-template <int NT>
+// KH waves share a row group and split its words (wave h of the group takes words 64 h + lane + 64 KH i); their sums
+// meet in LDS in wave order. Block: 4 waves = 4 / KH row groups of 4 rows.
+template <int NT, int KH = 1>
 __global__ __launch_bounds__(256) void tern_rows_kernel(TernArgs a) {
     constexpr int R = TERN_ROWS_WAVE;
-    const int lane = threadIdx.x & 63;
-    const int r0g = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-    if (r0g >= a.rows) return;  // no barriers below
-    int r0 = r0g;
+    __shared__ float red[KH > 1 ? 4 : 1][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kh = wave % KH;
+    const int r0g = (blockIdx.x * (4 / KH) + wave / KH) * R;
+    const bool live = r0g < a.rows;
+    if (KH == 1 && !live) return;  // no barriers below when KH == 1
+    int r0 = live ? r0g : 0;
     const int mi = tern_member(a, r0);
     const TernMat m = tern_mat(a, mi);
     const int K = a.K, kw = K >> 4, kg = K >> 7;
@@ -126,8 +130,9 @@ __global__ __launch_bounds__(256) void tern_rows_kernel(TernArgs a) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) xn[t][q] = reinterpret_cast<const f4*>(a.x + (int64_t)t * a.x_ts + 16 * j)[q];
     };
-    if (lane < kw) load(lane);
-    for (int j = lane; j < kw; j += 64) {
+    const int jl = 64 * kh + lane;
+    if (jl < kw) load(jl);
+    for (int j = jl; j < kw; j += 64 * KH) {
         uint32_t wc[R];
         float sc[R], xv[NT][16], xs[NT];
 #pragma unroll
@@ -147,7 +152,7 @@ __global__ __launch_bounds__(256) void tern_rows_kernel(TernArgs a) {
                 }
             xs[t] = s;
         }
-        if (j + 64 < kw) load(j + 64);
+        if (j + 64 * KH < kw) load(j + 64 * KH);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             // code e = 4b + s sits in byte b of (wd >> 2s) & 0x03030303 (one v_cvt_f32_ubyte per code)
@@ -174,6 +179,13 @@ __global__ __launch_bounds__(256) void tern_rows_kernel(TernArgs a) {
         const float v[4] = {acc[0][t], acc[1][t], acc[2][t], acc[3][t]};
         const float sum = wave_sum4(v, lane);
         if ((lane & 15) == t) mine = sum;
+    }
+    if constexpr (KH > 1) {
+        red[wave][lane] = mine;
+        __syncthreads();
+        if (!live || kh != 0) return;
+#pragma unroll
+        for (int h = 1; h < KH; ++h) mine += red[wave + h][lane];
     }
     if ((lane & 15) < NT) tern_store(a, m, mi, lane & 15, r0 + (lane >> 4), mine);
 }
