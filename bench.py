@@ -518,7 +518,7 @@ def main():
         line["roofline"] = {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                             "traffic_source": src,
-                            "kernel": "bn::decode_split_kernel<2> + bn::decode_combine_kernel (one library call, "
+                            "kernel": "bn::decode_split_kernel<2, false> + bn::decode_combine_kernel (one library call, "
                                       "timed as a whole; profiles/attn_kernels_all_workloads_trace.md has each)",
                             "algorithmic_bytes": head["bytes"]}
     pre = res.get("prefill_4k")
