@@ -2,8 +2,9 @@
 
 model.rs:690-707 then 815-894: norm_rotate (hidden rows -> the projections' input) -> q/k/v ternary projections ->
 attn_prep + attention + gate + Hadamard rotation (bn_attn_layer) -> o_proj added into the hidden rows. 2B layer
-shapes (hidden 2048, 8 query heads, 2 KV heads). Checked: the new hidden rows within max-abs 2e-3 of the oracle's,
-the appended K and V rows within one fp16 ulp (plus 1e-6). Also bn_norm_rotate alone against the oracle.
+shapes (hidden 2048, 8 query heads, 2 KV heads) and 4B (hidden 2560, 16 query heads, 4 KV heads). Checked: the new
+hidden rows within max-abs 2e-3 of the oracle's, the appended K and V rows within one fp16 ulp (plus 2e-5). Also
+bn_norm_rotate alone against the oracle, on both of its kernels.
 """
 import numpy as np
 import pytest
