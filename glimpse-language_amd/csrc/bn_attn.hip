@@ -15,6 +15,7 @@
 #include "bn_prep.h"
 #include "bn_ternary.h"
 #include "bn_util_kernels.h"
+#include "bn_verify.h"
 
 struct bn_ctx {
     int device;
@@ -28,6 +29,8 @@ struct bn_ctx {
     int decode_target_waves;
     // splits of one sequence at most (1 .. kMaxSplitsCap; BONSAI_ATTN_DECODE_MAX_SPLITS)
     int decode_max_splits;
+    // 2..8 verify rows on verify_kernel (1, the default) or as decodes of their rows (0; BONSAI_ATTN_VERIFY_MFMA)
+    int verify_mfma;
     char err[256];
 };
 
@@ -355,6 +358,89 @@ bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, const bn:
     return launch_decode(ctx, st, d, p);
 }
 
+#ifndef BN_VERIFY_WAVES
+#define BN_VERIFY_WAVES 4
+#endif
+#ifndef BN_VERIFY_BLOCKS
+#define BN_VERIFY_BLOCKS 256
+#endif
+constexpr int kVerifyMfmaMax = 8;  // 4 heads x 8 rows: one 32-column MFMA tile
+
+// verify_kernel's keys per split for 2..8 rows: about BN_VERIFY_BLOCKS blocks over the kv heads, whole 32-key tiles
+// for each of the W waves, and never more splits than the workspace query sized (its chunk is a lower bound).
+// 0 when the workspace holds no partials (a short context: every row fits one split of the decode path).
+int64_t verify_chunk(const bn_attn_args* a) {
+    if (a->T < 2 || a->T > (uint32_t)kVerifyMfmaMax) return 0;
+    const int64_t T = a->T, off = a->off, nk = off + T;
+    const DecodePlan ws = plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap);
+    if (!ws.multi) return 0;
+    const int64_t sum = T * (off + 1) + T * (T - 1) / 2;
+    const int64_t ws_chunk = bn::dec_chunk(sum, (int)ws.target, (int)nk, (int)ws.max_splits);
+    const int64_t step = 32 * BN_VERIFY_WAVES;
+    int64_t c = ceil_div(nk * a->KV, BN_VERIFY_BLOCKS);
+    if (c < ws_chunk) c = ws_chunk;
+    return ceil_div(c, step) * step;
+}
+
+// bn_attn_layer's fp16 q rows for verify_kernel when the caller gives no q output: after the partials in the
+// workspace (256-byte aligned), T x H x 256 fp16
+size_t verify_q_offset(const bn_attn_args* a) {
+    return (plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap).total() + 255) / 256 * 256;
+}
+
+// 2..8 rows of one sequence on verify_kernel (every K/V row read once for all rows), then decode_combine_kernel
+// for the merge, the gate and the rotation. The rows' K/V are appended first when given.
+bn_status run_verify(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int64_t chunk) {
+    if (a->k_new) {
+        bn_status s = launch_append(ctx, st, a);
+        if (s) return s;
+    }
+    const int64_t T = a->T, nk = (int64_t)a->off + T, ns = ceil_div(nk, chunk);
+    const int64_t units = 8 * T * ceil_div(ns, 8);
+    bn::VerifyArgs v{};
+    if (a->flags & BN_Q_F16)
+        v.q16 = static_cast<const uint16_t*>(a->q);
+    else
+        v.q = static_cast<const float*>(a->q);
+    v.q_ts = a->q_ts;
+    v.q_hs = a->q_hs;
+    v.kc = a->kc;
+    v.vc = a->vc;
+    v.part = static_cast<float*>(a->ws);
+    v.T = (int)T;
+    v.off = (int)a->off;
+    v.KV = (int)a->KV;
+    v.chunk = (int)chunk;
+    v.units = (int)units;
+    hipLaunchKernelGGL(bn::verify_kernel<BN_VERIFY_WAVES>, dim3((unsigned)ns, (unsigned)a->KV),
+                       dim3(64 * BN_VERIFY_WAVES), 0, st, v);
+    bn_status s = launched(ctx, "verify_kernel");
+    if (s) return s;
+    bn::DecodeArgs d{};
+    d.kc = a->kc;
+    d.vc = a->vc;
+    d.len0 = (int32_t)a->off + 1;
+    d.len_step = 1;
+    d.gate = a->gate;
+    d.g_ss = a->g_ts;
+    d.g_hs = a->g_hs;
+    d.out = a->out;
+    d.o_ss = a->o_ts;
+    d.o_hs = a->o_hs;
+    d.signs = a->signs;
+    d.KV = (int)a->KV;
+    d.nseq = (int)T;
+    d.max_len = (int)nk;
+    d.target = 1;
+    d.max_splits = (int)ns;
+    d.units = (int)units;
+    d.xcd_rows = 1;
+    d.chunk = (int)chunk;
+    d.part = v.part;
+    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3((unsigned)T, (unsigned)(2 * a->KV)), dim3(512), 0, st, d);
+    return launched(ctx, "decode_combine_kernel");
+}
+
 bn_status run_prefill(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     bn::PrefillArgs f{};
     if (a->flags & BN_Q_F16)
@@ -671,6 +757,10 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
 // kind: 0 forward, 1 decode, 2 verify, 3 prefill. One row is always a decode; verify-sized calls (T <= 16) of the
 // forward and verify entry points run as decodes of their rows; the rest take the MFMA prefill kernels.
 bn_status run(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int kind) {
+    if (kind != 3 && ctx->verify_mfma) {
+        const int64_t chunk = verify_chunk(a);
+        if (chunk) return run_verify(ctx, st, a, chunk);
+    }
     if (a->T == 1 || (kind != 3 && a->T <= (uint32_t)kVerifyMax)) return run_rows(ctx, st, a);
     return run_flash(ctx, st, a);
 }
@@ -724,6 +814,8 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
         const int v = atoi(e);
         if (v >= 1 && v <= kMaxSplitsCap) c->decode_max_splits = v;
     }
+    c->verify_mfma = 1;
+    if (const char* e = getenv("BONSAI_ATTN_VERIFY_MFMA")) c->verify_mfma = atoi(e) != 0;
     c->err[0] = 0;
     *out = c;
     return BN_OK;
@@ -735,7 +827,8 @@ const char* bn_ctx_last_error(const bn_ctx* ctx) { return ctx ? ctx->err : g_che
 
 size_t bn_attn_workspace_size(const bn_attn_args* a) {
     if (!a || a->KV < 1 || a->T < 1) return 0;
-    const size_t rows = a->T <= (uint32_t)kVerifyMax ? plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap).total() : 0;
+    size_t rows = a->T <= (uint32_t)kVerifyMax ? plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap).total() : 0;
+    if (verify_chunk(a)) rows = verify_q_offset(a) + (size_t)a->T * a->H * bn::D * sizeof(uint16_t);
     if (a->T == 1) return rows;
     // the kernel choice for T >= 2 depends on the context, so the size covers the flash kernel's partials
     const size_t fl = plan_flash(a->T, a->off, a->KV).total();
@@ -933,6 +1026,27 @@ bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, co
     rp.s1 = (int)p->s1;
     rp.s2 = (int)p->s2;
     if (p->T <= (uint32_t)kVerifyMax) {
+        // 2..8 rows: prep_kernel writes q (to p->q, else fp16 into the workspace after the partials) and the K/V
+        // rows, then verify_kernel and the merge
+        const int64_t chunk = ctx->verify_mfma ? verify_chunk(&m) : 0;
+        if (chunk) {
+            bn_prep_args pq = *p;
+            if (!pq.q) {
+                pq.q = static_cast<char*>(m.ws) + verify_q_offset(&m);
+                pq.flags = BN_Q_F16;
+                pq.q_ts = (int64_t)p->H * bn::D;
+                pq.q_hs = bn::D;
+            }
+            s = launch_prep(ctx, st, &pq, false);
+            if (s) return s;
+            m.k_new = nullptr;
+            m.v_new = nullptr;
+            m.q = pq.q;
+            m.q_ts = pq.q_ts;
+            m.q_hs = pq.q_hs;
+            m.flags = pq.flags;
+            return run_verify(ctx, st, &m, chunk);
+        }
         // decode / verify rows: q normed and rotated in the split kernel's prologue; one row also appends its
         // K/V row there, several rows have theirs written by prep_kernel first
         if (p->T > 1) {

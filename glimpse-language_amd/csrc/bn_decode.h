@@ -64,6 +64,8 @@ struct DecodeArgs {
     int units;           // launch width per kv head (>= sum_i n_i)
     int xcd_rows;        // rows of one sequence (verify): unit 8 (t + T (s / 8)) + s % 8 is split s of row t, so the
                          // same split of every row runs on one XCD and shares its K/V rows through that L2
+    int chunk;           // nonzero: keys per split, fixed by verify_kernel, which writes a record for every row and
+                         // split (decode_combine_kernel then also merges rows of one split)
 };
 
 constexpr int DEC_MIN_CHUNK = 64;
@@ -120,7 +122,7 @@ __device__ DecSplit dec_find_unit(const DecodeArgs& a, int b, int lane) {
     const int L0 = lane < a.nseq ? dec_len(a, lane) : 0;  // the first 64 lengths stay in registers
     int64_t tot = L0;
     for (int base = 64; base < a.nseq; base += 64) tot += base + lane < a.nseq ? dec_len(a, base + lane) : 0;
-    r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len, a.max_splits);
+    r.chunk = a.chunk ? a.chunk : dec_chunk(wave_sum64(tot), a.target, a.max_len, a.max_splits);
     r.seq = -1;
     r.P = r.n = r.L = r.s = 0;
     if (a.xcd_rows) {
@@ -161,7 +163,7 @@ __device__ DecSplit dec_find_seq(const DecodeArgs& a, int seq, int lane) {
     const int L0 = lane < a.nseq ? dec_len(a, lane) : 0;
     int64_t tot = L0;
     for (int base = 64; base < a.nseq; base += 64) tot += base + lane < a.nseq ? dec_len(a, base + lane) : 0;
-    r.chunk = dec_chunk(wave_sum64(tot), a.target, a.max_len, a.max_splits);
+    r.chunk = a.chunk ? a.chunk : dec_chunk(wave_sum64(tot), a.target, a.max_len, a.max_splits);
     r.seq = seq;
     r.s = 0;
     if (a.xcd_rows) {
@@ -518,7 +520,7 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i = wave >> 2, q = wave & 3, d0 = lane * 4;
     const DecSplit sp = dec_find_seq(a, seq, lane);
     const int ns = sp.n;
-    if (ns <= 1) return;  // written by the split kernel
+    if (ns <= 1 && !a.chunk) return;  // written by the split kernel
     const int h = 2 * j + i, head = kh * 4 + h;
     // the record of this wave's k-th split (split q + 4k)
     auto rec = [&](int k) -> const float* {

@@ -1,0 +1,227 @@
+// Speculative verify on fp16 MFMA: 2..8 draft rows of one sequence against the cache, every K/V row read once
+// for all rows.
+//
+// Semantics follow attn_split.comp:9-58 + attn_combine.comp:6-21 of the reference: row t (position off+t) of head
+// h attends to cache rows [0, off+t+1) of kv head h/4 (causal among the drafts), softmax(q.k/16) v. The K/V rows
+// of the call are in the cache before this kernel runs. The gate and the rotation are decode_combine_kernel's.
+//
+// Decomposition (this kernel's own):
+//   The 4 query heads of a kv head times T <= 8 rows are at most 32 query rows: one MFMA column tile. Column
+//   c = 8 hq + t holds row t of head 4 kh + hq (columns t >= T repeat row T-1 and are dropped). Block (split s,
+//   kv head kh) covers keys [s chunk, (s+1) chunk) for all 32 columns; its W waves take contiguous runs of the
+//   split's 32-key tiles, each wave with its own K/V stage in LDS (the tile layout of prefill_kernel: rows p and
+//   p+16 share one 1 KB global_load_lds copy, padded so the operand reads are conflict-free).
+//   S^T = K Q^T on v_mfma_f32_32x32x16_f16 (Q^T in registers as fp16), online softmax in fp32 in the log2
+//   domain (the running max moves only when a column's max grows by more than 2^8), O += P V with P from the
+//   S^T registers and V from ds_read_b64_tr_b16 reads, as in prefill_kernel.
+//   The block merges its W waves in wave order through LDS and writes one partial record (m, l, acc) per row and
+//   split in decode_combine_kernel's layout (m in the log2 domain, slot 8 (t + T (s / 8)) + s % 8); the combine
+//   merges every row's splits in split order, so results are reproducible bit for bit.
+#pragma once
+#include "bn_decode.h"
+#include "bn_prefill.h"
+
+namespace bn {
+
+struct VerifyArgs {
+    const float* q;          // element t*q_ts + h*q_hs + d (fp32) ...
+    const uint16_t* q16;     // ... or fp16 bits when non-null
+    int64_t q_ts, q_hs;
+    const uint16_t* kc;      // fp16 [rows][KV][256]
+    const uint16_t* vc;
+    float* part;             // [KV][units][DEC_PART]
+    int T, off, KV, chunk, units;
+};
+
+constexpr int VF_OP = 1040;  // row pitch (bytes) of a wave's O rows in LDS at the merge
+
+template <int W>
+__global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[W * PF_STAGE];
+    __shared__ float ml_lds[W][2][32];  // per wave: m, l of each column
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, r32 = lane & 31;
+    const int s = blockIdx.x, kh = blockIdx.y, KV = a.KV, T = a.T;
+    const int nk = a.off + T;                            // cache rows that exist
+    const int k0 = s * a.chunk;
+    const int k1 = min(k0 + a.chunk, nk);
+    const int nt = (k1 - k0 + PF_BK - 1) / PF_BK;        // the split's 32-key tiles
+    const int j_begin = w * nt / W, j_end = (w + 1) * nt / W;
+    const int64_t kvd = (int64_t)KV * D;
+    const uint16_t* kb = a.kc + (int64_t)kh * D;
+    const uint16_t* vb = a.vc + (int64_t)kh * D;
+    uint8_t* const st = lds + w * PF_STAGE;
+
+    // this lane's column: row t of head 4 kh + hq; its keys are <= qpos
+    const int hq = r32 >> 3, t = min(r32 & 7, T - 1);
+    const int qpos = a.off + t;
+
+    // Q^T operand: lane holds column r32, dims 16 ks + 8 h .. +7, fp16 (nearest even)
+    h8 qb[16];
+    if (a.q16) {
+        const uint16_t* qr = a.q16 + (int64_t)t * a.q_ts + (int64_t)(kh * 4 + hq) * a.q_hs + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) qb[ks] = ld_h8(qr + 16 * ks);
+    } else {
+        const float* qr = a.q + (int64_t)t * a.q_ts + (int64_t)(kh * 4 + hq) * a.q_hs + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) qb[ks] = ld_f32x8_as_h8(qr + 16 * ks);
+    }
+
+    // Tile copy into this wave's stage: instruction i moves row pair i (rows i, i+16) of K and of V; lane l
+    // loads row i + 16 (l/32), 16-byte chunk l%32, into LDS pair i at byte 16 l. Rows past the cache's last row
+    // are clamped to it (their scores are masked: every column's qpos < nk).
+    const uint32_t lane_go = (uint32_t)(16 * h * (int)kvd + r32 * 8) * 2u;
+    auto issue_tile = [&](int j) {
+        const int j0 = k0 + j * PF_BK;
+        if (j0 + PF_BK <= nk) {
+            const char* kt = reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd);
+            const char* vt = reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                __builtin_amdgcn_global_load_lds(kt + i * kvd * 2 + lane_go, (pf_lds_void_t*)(st + i * PF_KP), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vt + i * kvd * 2 + lane_go, (pf_lds_void_t*)(st + PF_KB + i * PF_VP),
+                                                 16, 0, 0);
+            }
+        } else {
+            const int lim = nk - 1 - j0;  // last valid row of this tile
+            const char* kt = reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd);
+            const char* vt = reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t go = (uint32_t)(min(i + 16 * h, lim) * (int)kvd + r32 * 8) * 2u;
+                __builtin_amdgcn_global_load_lds(kt + go, (pf_lds_void_t*)(st + i * PF_KP), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vt + go, (pf_lds_void_t*)(st + PF_KB + i * PF_VP), 16, 0, 0);
+            }
+        }
+    };
+
+    f16x o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float sc = QK_SCALE * LOG2E;
+    const int k_lane = (r32 & 15) * PF_KP + (r32 >> 4) * 512 + h * 16;
+    const int vs = lane & 15, vnh = (lane >> 4) & 1;
+    const int v_lane = PF_KB + (4 * h + (vs >> 2)) * PF_VP + 32 * vnh + 8 * (vs & 3);
+    __shared__ f4 bc_lds[W][16];
+    float* bc = reinterpret_cast<float*>(bc_lds[w]);
+
+    for (int j = j_begin; j < j_end; j++) {
+        issue_tile(j);
+        pf_wait_vm0();
+        wave_lds_sync();  // the tile is in this wave's stage
+        const uint8_t* kl = st + k_lane;
+        const uint8_t* vl = st + v_lane;
+        const int j0 = k0 + j * PF_BK;
+        f16x sv;
+#pragma unroll
+        for (int r = 0; r < 16; r++) sv[r] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) sv = mfma32(pf_lds_h8(kl + ks * 32), qb[ks], sv);
+        // causal mask where a key may pass a column's position; register r holds key j0 + 8(r/4) + 4h + r%4
+        if (j0 + PF_BK - 1 > a.off) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                sv[r] = key <= qpos ? sv[r] : -INFINITY;
+            }
+        }
+        float tm = sv[0];
+#pragma unroll
+        for (int r = 1; r < 16; r++) tm = fmaxf(tm, sv[r]);
+        tm = max_xhalf(tm);
+        const float tmax = tm * sc;
+        float alpha = 1.0f;
+        bool moved = false;
+        if (tmax > m_run + 8.0f) {
+            moved = m_run != -INFINITY;
+            alpha = moved ? __builtin_amdgcn_exp2f(m_run - tmax) : 0.0f;
+            m_run = tmax;
+        }
+        if (__ballot(moved)) {
+            if (h == 0) bc[r32] = alpha;
+            wave_lds_sync();
+            f4 al[4];
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) al[gg] = bc_lds[w][2 * gg + h];
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[dt][r] *= al[r >> 2][r & 3];
+        }
+        l_run *= alpha;
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        h8 pa[2];
+#pragma unroll
+        for (int r = 0; r < 16; r++) pa[r >> 3][r & 7] = (_Float16)__builtin_amdgcn_exp2f(fmaf(sv[r], sc, -m_use));
+        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const h2 pp = {pa[k][2 * e], pa[k][2 * e + 1]};
+                l_run = __builtin_amdgcn_fdot2(pp, one, l_run, false);
+            }
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const int imm0 = kk * 512 + 64 * dt;
+                const h4 x0 = pf_lds_tr(vl + imm0);
+                const h4 x1 = pf_lds_tr(vl + imm0 + 8 * PF_VP);
+                const h8 vop = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[dt] = mfma32(pa[kk], vop, o[dt]);
+            }
+        }
+        wave_lds_sync();  // every read of the stage is done before the next tile's copy
+    }
+
+    // Merge in wave order. Each wave leaves (m, l) per column and its O rows (column c: row c, dims at 4 d,
+    // pitch VF_OP) in its own stage; then the block sums the waves' O scaled by 2^(m_w - M) and writes the
+    // records of the columns that are real rows with keys in this split.
+    const float l_tot = sum_xhalf(l_run);
+    if (h == 0) {
+        ml_lds[w][0][r32] = m_run;
+        ml_lds[w][1][r32] = l_tot;
+    }
+    // O register r of tile dt: column 8(r/4) + 4h + r%4, dim 32 dt + r32
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int c = 8 * (r >> 2) + 4 * h + (r & 3);
+            *reinterpret_cast<float*>(st + c * VF_OP + 4 * (32 * dt + r32)) = o[dt][r];
+        }
+    __syncthreads();
+    for (int e = tid; e < 32 * 64; e += 64 * W) {
+        const int c = e >> 6, d4 = e & 63, tc = c & 7, hc = c >> 3;
+        if (tc >= T || k0 > a.off + tc) continue;
+        float M = ml_lds[0][0][c];
+#pragma unroll
+        for (int v = 1; v < W; v++) M = fmaxf(M, ml_lds[v][0][c]);
+        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        float L = 0.0f;
+#pragma unroll
+        for (int v = 0; v < W; v++) {
+            const float mv = ml_lds[v][0][c];
+            const float f = mv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv - M);
+            L = fmaf(ml_lds[v][1][c], f, L);
+            const f4 x = *reinterpret_cast<const f4*>(lds + v * PF_STAGE + c * VF_OP + 16 * d4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = fmaf(x[i], f, acc[i]);
+        }
+        float* rec = a.part + ((int64_t)kh * a.units + 8 * (tc + T * (s >> 3)) + (s & 7)) * DEC_PART;
+        *reinterpret_cast<f4*>(rec + 8 + hc * D + 4 * d4) = acc;
+        if (d4 == 0) {
+            rec[hc] = M;
+            rec[4 + hc] = L;
+        }
+    }
+}
+
+}  // namespace bn

@@ -109,9 +109,17 @@ def test_verify_8_workload(gpu):
     check_case(gpu, inp, ba.KIND_VERIFY)
 
 
-@pytest.mark.parametrize("T,off", [(2, 0), (3, 17), (16, 1000), (5, 4095)])
+# (2, 0), (3, 17): short contexts, rows as decodes of one split; (16, 1000): more rows than one MFMA tile holds;
+# the rest run on verify_kernel: one split (2, 63), a partial last tile (6, 129), many splits
+@pytest.mark.parametrize("T,off", [(2, 0), (3, 17), (16, 1000), (5, 4095), (2, 63), (6, 129), (7, 1000), (8, 9000)])
 def test_verify_shapes(gpu, T, off):
     inp = workload.layer(900 + T + off, T=T, off=off, H=8, KV=2)
+    check_case(gpu, inp, ba.KIND_VERIFY)
+
+
+@pytest.mark.parametrize("T,off,gate", [(8, 8191, True), (3, 2000, False), (4, 250, True)])
+def test_verify_4b_heads(gpu, T, off, gate):
+    inp = workload.layer(950 + T + off, T=T, off=off, H=16, KV=4, gate=gate)
     check_case(gpu, inp, ba.KIND_VERIFY)
 
 
@@ -129,6 +137,21 @@ def test_verify_rows_equal_decodes(gpu):
                          gate=d["gate"][t:t + 1], kind=ba.KIND_DECODE)
         torch.cuda.synchronize()
         assert np.max(np.abs(o.cpu().numpy()[0] - out[t])) <= 2e-4
+
+
+def test_verify_kernel_equals_rows_path(gpu):
+    """verify_kernel (all rows of a kv head in one MFMA tile, each K/V row read once) against the same call run as
+    decodes of its rows (BONSAI_ATTN_VERIFY_MFMA=0): both carry the reference's semantics, and differ only by the
+    fp16 rounding of q in the MFMA scores (a few 1e-5); 2e-4 bounds it."""
+    from conftest import context_with
+    torch, ctx, ws = gpu
+    inp = workload.layer(0x9500, T=8, off=8184, H=16, KV=4)
+    out, d = run(gpu, inp, ba.KIND_VERIFY)
+    ctx0 = context_with(BONSAI_ATTN_VERIFY_MFMA=0)
+    ws0 = ba.Workspace(ctx0, "cuda")
+    rows = ba.attention(ctx0, ws0, d["q"], d["kc"], d["vc"], inp["off"], gate=d["gate"], kind=ba.KIND_VERIFY)
+    torch.cuda.synchronize()
+    assert np.max(np.abs(rows.cpu().numpy() - out)) <= 2e-4
 
 
 def test_prefill_prefix_workload(gpu):
