@@ -362,7 +362,7 @@ bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, const bn:
 #define BN_VERIFY_WAVES 4
 #endif
 #ifndef BN_VERIFY_BLOCKS
-#define BN_VERIFY_BLOCKS 256
+#define BN_VERIFY_BLOCKS 128
 #endif
 constexpr int kVerifyMfmaMax = 8;  // 4 heads x 8 rows: one 32-column MFMA tile
 

@@ -58,18 +58,6 @@ __global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
     const int hq = r32 >> 3, t = min(r32 & 7, T - 1);
     const int qpos = a.off + t;
 
-    // Q^T operand: lane holds column r32, dims 16 ks + 8 h .. +7, fp16 (nearest even)
-    h8 qb[16];
-    if (a.q16) {
-        const uint16_t* qr = a.q16 + (int64_t)t * a.q_ts + (int64_t)(kh * 4 + hq) * a.q_hs + 8 * h;
-#pragma unroll
-        for (int ks = 0; ks < 16; ks++) qb[ks] = ld_h8(qr + 16 * ks);
-    } else {
-        const float* qr = a.q + (int64_t)t * a.q_ts + (int64_t)(kh * 4 + hq) * a.q_hs + 8 * h;
-#pragma unroll
-        for (int ks = 0; ks < 16; ks++) qb[ks] = ld_f32x8_as_h8(qr + 16 * ks);
-    }
-
     // Tile copy into this wave's stage: instruction i moves row pair i (rows i, i+16) of K and of V; lane l
     // loads row i + 16 (l/32), 16-byte chunk l%32, into LDS pair i at byte 16 l. Rows past the cache's last row
     // are clamped to it (their scores are masked: every column's qpos < nk).
@@ -111,8 +99,22 @@ __global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
     __shared__ f4 bc_lds[W][16];
     float* bc = reinterpret_cast<float*>(bc_lds[w]);
 
+    // the first tile's copy is in flight while the q rows load
+    if (j_begin < j_end) issue_tile(j_begin);
+    // Q^T operand: lane holds column r32, dims 16 ks + 8 h .. +7, fp16 (nearest even)
+    h8 qb[16];
+    if (a.q16) {
+        const uint16_t* qr = a.q16 + (int64_t)t * a.q_ts + (int64_t)(kh * 4 + hq) * a.q_hs + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) qb[ks] = ld_h8(qr + 16 * ks);
+    } else {
+        const float* qr = a.q + (int64_t)t * a.q_ts + (int64_t)(kh * 4 + hq) * a.q_hs + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < 16; ks++) qb[ks] = ld_f32x8_as_h8(qr + 16 * ks);
+    }
+
     for (int j = j_begin; j < j_end; j++) {
-        issue_tile(j);
+        if (j > j_begin) issue_tile(j);
         pf_wait_vm0();
         wave_lds_sync();  // the tile is in this wave's stage
         const uint8_t* kl = st + k_lane;
