@@ -107,7 +107,8 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, int t, int hh, f4 x,
 
 constexpr int PREP_B = 4;  // head rows per wave with their loads in flight together
 
-// Grid (T) x 4 waves: block = token t; wave w takes head rows h_first + w, + 4, + 8, ..., PREP_B of them at a
+// Grid (T, G) x 4 waves: block (t, y) = token t; wave w takes head rows h_first + 16 y + w, + 4, + 8, + 12, then
+// the same 16 rows further on by 16 G (G > 1 splits a few tokens' rows over more CUs), PREP_B of them at a
 // time with all their loads issued before the first is used (one row per wave left too few bytes in flight per
 // CU to reach the HBM rate). h_first = H when no q output is asked for (K/V rows only). The norm weights and the
 // token's sin/cos are fetched once per wave, before the rows.
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a) {
     const f4 wk = *reinterpret_cast<const f4*>(a.rp.kn + d0);
     f4 cs, sn;
     rope_angles(a.rp, t, d0, cs, sn);
-    for (int h0 = h_first + wave; h0 < nh; h0 += 4 * PREP_B) {
+    for (int h0 = h_first + wave + 4 * PREP_B * (int)blockIdx.y; h0 < nh; h0 += 4 * PREP_B * (int)gridDim.y) {
         f4 x[PREP_B];
 #pragma unroll
         for (int b = 0; b < PREP_B; b++) {
