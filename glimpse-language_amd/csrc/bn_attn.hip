@@ -14,6 +14,7 @@
 #include "bn_flash.h"
 #include "bn_prefill.h"
 #include "bn_prefill_hilo.h"
+#include "bn_prefill_pair.h"
 #include "bn_prep.h"
 #include "bn_ternary.h"
 #include "bn_ternary_pf.h"
@@ -37,6 +38,8 @@ struct bn_ctx {
     int flash_target_blocks;
     // 2..8 verify rows on verify_kernel (1, the default) or as decodes of their rows (0; BONSAI_ATTN_VERIFY_MFMA)
     int verify_mfma;
+    // fp16-q prefills on prefill_kernel (0, the default) or prefill_pair_kernel (1; BONSAI_ATTN_PREFILL_PAIR=1)
+    int prefill_pair;
     // this device's copy of `scratch` (the partials of bn_attn_decode_ragged_noalloc), or null if its address
     // could not be taken
     void* scratch;
@@ -541,6 +544,10 @@ bn_status run_prefill(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     f.KV = (int)a->KV;
     f.ntq = (int)ceil_div(a->T, bn::PF_BQ);
     const int64_t blocks = (int64_t)a->KV * f.ntq;
+    if (f.q16 && ctx->prefill_pair) {
+        hipLaunchKernelGGL(bn::prefill_pair_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
+        return launched(ctx, "prefill_pair_kernel");
+    }
     if (f.q16) {
         hipLaunchKernelGGL(bn::prefill_kernel, dim3((unsigned)blocks), dim3(512), 0, st, f);
         return launched(ctx, "prefill_kernel");
@@ -991,6 +998,8 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
     }
     c->verify_mfma = 1;
     if (const char* e = getenv("BONSAI_ATTN_VERIFY_MFMA")) c->verify_mfma = atoi(e) != 0;
+    c->prefill_pair = 0;
+    if (const char* e = getenv("BONSAI_ATTN_PREFILL_PAIR")) c->prefill_pair = atoi(e) != 0;
     c->scratch = scratch_address(device);
     c->err[0] = 0;
     *out = c;

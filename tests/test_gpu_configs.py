@@ -6,7 +6,8 @@ projected reference values tie within 1e-4 relative are not compared). Cache row
 bit for bit.
   - decode_8k_batch32: 32 sequences x 8192 fp16 KV rows, 16 query / 4 kv heads, append + gate (the headline);
   - ragged_32: 32 sequences with lengths from random.Random(0xB0A5A104) in [1024, 32768] (sum 507,255);
-  - prefill_4k: all 4096 rows of the causal prefill with fp16 q (BN_Q_F16), 16/4 heads.
+  - prefill_4k: all 4096 rows of the causal prefill, 16/4 heads, with fp16 q (BN_Q_F16; prefill_kernel and
+    prefill_pair_kernel) and with fp32 q (prefill_hilo_kernel).
 The peaky cases multiply the RMS-normalised q and k rows by a norm weight w (scores q.k/16 then have standard
 deviation w^2: tens at w = 4..8), where rounding q to fp16 in an MFMA kernel would move a score by about 1e-4 w^2.
 """
@@ -64,21 +65,42 @@ def test_ragged_32_as_benchmarked(gpu):
     ragged_case(gpu, lens, 0xB0A5A105)
 
 
-def test_prefill_4k_all_rows_fp16_q(gpu):
-    torch, ctx, ws = gpu
+def prefill_4k_case(gpu, q_f16, ctx=None):
+    torch, ctx0, ws0 = gpu
+    ctx = ctx or ctx0
+    ws = ws0 if ctx is ctx0 else ba.Workspace(ctx, "cuda")
     H, KV, T, off = 16, 4, 4096, 0
-    x = bench.attn_inputs(torch, H, KV, T, off, 0xB0A5A103, q_f16=True)
-    print("prefill_4k parity: 4096 rows, 16/4 heads, fp16 q", flush=True)
+    x = bench.attn_inputs(torch, H, KV, T, off, 0xB0A5A103, q_f16=q_f16)
+    print(f"prefill_4k parity: 4096 rows, 16/4 heads, {'fp16' if q_f16 else 'fp32'} q", flush=True)
     kc0, vc0 = host(x["kc"]).view(np.uint16).copy(), host(x["vc"]).view(np.uint16).copy()
     out = ba.attention(ctx, ws, x["q"], x["kc"], x["vc"], off, k_new=x["k_new"], v_new=x["v_new"], gate=x["gate"],
                        kind=ba.KIND_PREFILL)
     torch.cuda.synchronize()
     oracle.append(host(x["k_new"]), host(x["v_new"]), kc0, vc0, off)
-    q32 = host(x["q"].float())  # the fp16 q the kernel read, exactly
+    q32 = host(x["q"].float())  # the q the kernel read, exactly
     ref = oracle.attend(q32, kc0, vc0, off, host(x["gate"]))
     err = assert_parity(host(out), ref, H, "prefill_4k")
     assert np.array_equal(cache_np(x["kc"]), kc0) and np.array_equal(cache_np(x["vc"]), vc0)
     print(f"prefill_4k parity: max-abs {err:.3e}", flush=True)
+
+
+def test_prefill_4k_all_rows_fp16_q(gpu):
+    prefill_4k_case(gpu, True)
+
+
+def test_prefill_4k_all_rows_fp16_q_pair_kernel(gpu):
+    """The same rows on prefill_pair_kernel (BONSAI_ATTN_PREFILL_PAIR=1)."""
+    ctx = context_with(BONSAI_ATTN_PREFILL_PAIR=1)
+    try:
+        prefill_4k_case(gpu, True, ctx)
+    finally:
+        gpu[0].cuda.synchronize()
+        ctx.close()
+
+
+def test_prefill_4k_all_rows_fp32_q(gpu):
+    """All 4096 rows with fp32 q (the reference's precision; prefill_hilo_kernel multiplies q as fp16 hi + lo)."""
+    prefill_4k_case(gpu, False)
 
 
 def peaky(seed, T, off, H, KV, w):

@@ -1,6 +1,7 @@
-"""Parity of the two long-prefill kernels with the oracle: prefill_kernel (fp16 q; 8 waves per block, key range
-split between two wave groups) and prefill_hilo_kernel (fp32 q as an fp16 hi/lo pair; one wave per SIMD, 4-stage
-copy ring).
+"""Parity of the long-prefill kernels with the oracle: prefill_kernel (fp16 q; 8 waves per block, key range
+split between two wave groups), prefill_pair_kernel (fp16 q; 4 waves per block, two query heads per wave; chosen with
+BONSAI_ATTN_PREFILL_PAIR=1) and prefill_hilo_kernel (fp32 q as an fp16 hi/lo pair; one wave per SIMD, 4-stage copy
+ring). Every test runs once per fp16-q kernel.
 
 By default the library sends a T >= 2 call to these kernels only when it gives at least as many 32-token q-tile
 blocks as the GPU has CUs (for example the 4096-row prefill); here a second context created with
@@ -21,10 +22,14 @@ from glimpse_language_amd import bonsai_attn as ba
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def pf(gpu):
+@pytest.fixture(scope="module", params=["prefill_kernel", "prefill_pair_kernel"])
+def pf(gpu, request):
+    """A context that sends every T >= 2 call to the prefill kernels; fp16-q calls on the kernel named by the param
+    (BONSAI_ATTN_PREFILL_PAIR), fp32-q calls on prefill_hilo_kernel either way."""
     torch, _, _ = gpu
-    ctx = context_with(BONSAI_ATTN_PREFILL_MIN_BLOCKS=1)
+    print(f"prefill kernel for fp16 q: {request.param}", flush=True)
+    ctx = context_with(BONSAI_ATTN_PREFILL_MIN_BLOCKS=1,
+                       BONSAI_ATTN_PREFILL_PAIR=int(request.param == "prefill_pair_kernel"))
     ws = ba.Workspace(ctx, "cuda")
     yield torch, ctx, ws
     torch.cuda.synchronize()
