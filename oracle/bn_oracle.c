@@ -146,7 +146,7 @@ static float dot4(const float* a, const float* b) {
  * part layout as the reference: part[((t*H + h)*ns + s)*258 + {0: m, 1: l, 2+d: acc}]. */
 static void split_unit(int kh, int s, int t, int off, int H, int KV, int chunk, int ns,
                        const float* q, int64_t q_ts, int64_t q_hs, const float* kf, const float* vf,
-                       float* part, float* sc /* [4*chunk] */) {
+                       float* part, float* sc /* [4*chunk] */, int p16) {
     const int D = BN_OR_D;
     int n = off + t + 1;
     int j0 = s * chunk, j1 = n < j0 + chunk ? n : j0 + chunk;
@@ -183,6 +183,7 @@ static void split_unit(int kh, int s, int t, int off, int H, int KV, int chunk, 
             float acc = 0.0f;
             for (int i = l; i < cnt; i += 32) {
                 float p = expf(sh[i] - m);
+                if (p16) p = bn_or_f16_to_f32(bn_or_f32_to_f16(p)); /* perturbed variant: fp16 probabilities */
                 sh[i] = p;
                 acc += p;
             }
@@ -231,7 +232,7 @@ static void combine_unit(int h, int t, int H, int ns, const float* part, const f
 
 static int attend_f(int T, int off, int H, int KV, int chunk, const float* q, int64_t q_ts, int64_t q_hs,
                     const float* kf, const float* vf, const float* z, int64_t z_ts, int64_t z_hs, float* out,
-                    int64_t o_ts, int64_t o_hs, int nthreads) {
+                    int64_t o_ts, int64_t o_hs, int nthreads, int p16) {
     if (T <= 0 || off < 0 || KV <= 0 || H != 4 * KV) return -1;
     if (chunk <= 0) chunk = T <= 16 ? 64 : 512;
     int n = off + T;
@@ -250,7 +251,7 @@ static int attend_f(int T, int off, int H, int KV, int chunk, const float* q, in
 #endif
         for (int u = 0; u < units; u++) {
             int kh = u % KV, s = (u / KV) % ns, t = u / (KV * ns);
-            split_unit(kh, s, t, off, H, KV, chunk, ns, q, q_ts, q_hs, kf, vf, part, sc);
+            split_unit(kh, s, t, off, H, KV, chunk, ns, q, q_ts, q_hs, kf, vf, part, sc, p16);
         }
         free(sc);
 #ifdef _OPENMP
@@ -267,6 +268,12 @@ static int attend_f(int T, int off, int H, int KV, int chunk, const float* q, in
 int bn_or_attend(int T, int off, int H, int KV, int chunk, const float* q, int64_t q_ts, int64_t q_hs,
                  const uint16_t* kc, const uint16_t* vc, const float* z, int64_t z_ts, int64_t z_hs, float* out,
                  int64_t o_ts, int64_t o_hs, int nthreads) {
+    return bn_or_attend_ex(T, off, H, KV, chunk, q, q_ts, q_hs, kc, vc, z, z_ts, z_hs, out, o_ts, o_hs, nthreads, 0);
+}
+
+int bn_or_attend_ex(int T, int off, int H, int KV, int chunk, const float* q, int64_t q_ts, int64_t q_hs,
+                    const uint16_t* kc, const uint16_t* vc, const float* z, int64_t z_ts, int64_t z_hs, float* out,
+                    int64_t o_ts, int64_t o_hs, int nthreads, int flags) {
     if (T <= 0 || off < 0 || KV <= 0 || H != 4 * KV) return -1;
     size_t n = (size_t)(off + T) * KV * BN_OR_D;
     float* kf = (float*)malloc(sizeof(float) * n);
@@ -278,7 +285,8 @@ int bn_or_attend(int T, int off, int H, int KV, int chunk, const float* q, int64
     }
     bn_or_f16_to_f32_n(kc, kf, n);
     bn_or_f16_to_f32_n(vc, vf, n);
-    int r = attend_f(T, off, H, KV, chunk, q, q_ts, q_hs, kf, vf, z, z_ts, z_hs, out, o_ts, o_hs, nthreads);
+    int r = attend_f(T, off, H, KV, chunk, q, q_ts, q_hs, kf, vf, z, z_ts, z_hs, out, o_ts, o_hs, nthreads,
+                     flags & BN_OR_P16);
     free(kf);
     free(vf);
     return r;
@@ -287,13 +295,19 @@ int bn_or_attend(int T, int off, int H, int KV, int chunk, const float* q, int64
 int bn_or_decode_ragged(int nseq, int H, int KV, int chunk, const float* q, int64_t q_ts, const uint16_t* kc,
                         const uint16_t* vc, const int64_t* kv_off, const int32_t* kv_len, const float* z,
                         int64_t z_ts, float* out, int64_t o_ts, int nthreads) {
+    return bn_or_decode_ragged_ex(nseq, H, KV, chunk, q, q_ts, kc, vc, kv_off, kv_len, z, z_ts, out, o_ts, nthreads, 0);
+}
+
+int bn_or_decode_ragged_ex(int nseq, int H, int KV, int chunk, const float* q, int64_t q_ts, const uint16_t* kc,
+                           const uint16_t* vc, const int64_t* kv_off, const int32_t* kv_len, const float* z,
+                           int64_t z_ts, float* out, int64_t o_ts, int nthreads, int flags) {
     for (int i = 0; i < nseq; i++) {
         if (kv_len[i] < 1) return -1;
         size_t row = (size_t)KV * BN_OR_D;
-        int r = bn_or_attend(1, kv_len[i] - 1, H, KV, chunk, q + (int64_t)i * q_ts, q_ts, BN_OR_D,
-                             kc + (size_t)kv_off[i] * row, vc + (size_t)kv_off[i] * row,
-                             z ? z + (int64_t)i * z_ts : NULL, z_ts, BN_OR_D, out + (int64_t)i * o_ts, o_ts,
-                             BN_OR_D, nthreads);
+        int r = bn_or_attend_ex(1, kv_len[i] - 1, H, KV, chunk, q + (int64_t)i * q_ts, q_ts, BN_OR_D,
+                                kc + (size_t)kv_off[i] * row, vc + (size_t)kv_off[i] * row,
+                                z ? z + (int64_t)i * z_ts : NULL, z_ts, BN_OR_D, out + (int64_t)i * o_ts, o_ts,
+                                BN_OR_D, nthreads, flags);
         if (r) return r;
     }
     return 0;

@@ -43,6 +43,10 @@ def lib():
     L.bn_or_attend.restype = I
     L.bn_or_decode_ragged.argtypes = [I, I, I, I, P, I64, P, P, P, P, P, I64, P, I64, I]
     L.bn_or_decode_ragged.restype = I
+    L.bn_or_attend_ex.argtypes = [I, I, I, I, I, P, I64, I64, P, P, P, I64, I64, P, I64, I64, I, I]
+    L.bn_or_attend_ex.restype = I
+    L.bn_or_decode_ragged_ex.argtypes = [I, I, I, I, P, I64, P, P, P, P, P, I64, P, I64, I, I]
+    L.bn_or_decode_ragged_ex.restype = I
     L.bn_or_prep.argtypes = [P] * 10 + [I] * 7
     L.bn_or_prep.restype = None
     L.bn_or_sincos.argtypes = [ctypes.c_float, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float)]
@@ -104,11 +108,12 @@ def _strides(a):
     return [s // a.itemsize for s in a.strides]
 
 
-def attend(q, kc, vc, off, gate=None, chunk=0, nthreads=0):
+def attend(q, kc, vc, off, gate=None, chunk=0, nthreads=0, p16=False):
     """Reference attention for T query rows at positions off..off+T-1 (cache rows [0, off+T) present).
 
     q, gate: float32 arrays [T][H][256] (any strides with unit innermost stride); kc, vc: uint16 fp16 bits
-    [>=off+T][KV][256]. Returns out [T][H][256] float32."""
+    [>=off+T][KV][256]. Returns out [T][H][256] float32. p16: the perturbed reference (every probability rounded
+    to fp16 before both sums; not the reference's arithmetic) that sizes the argmax tie margins."""
     T, H = q.shape[0], q.shape[1]
     KV = kc.shape[1]
     assert q.strides[2] == 4 and kc.flags.c_contiguous and vc.flags.c_contiguous
@@ -117,14 +122,14 @@ def attend(q, kc, vc, off, gate=None, chunk=0, nthreads=0):
     gs = _strides(gate) if gate is not None else [0, 0, 0]
     if gate is not None:
         assert gate.dtype == np.float32 and gate.strides[2] == 4
-    r = lib().bn_or_attend(T, off, H, KV, chunk, _p(q), qs[0], qs[1], _p(kc), _p(vc), _p(gate), gs[0], gs[1],
-                           _p(out), H * D, D, nthreads)
+    r = lib().bn_or_attend_ex(T, off, H, KV, chunk, _p(q), qs[0], qs[1], _p(kc), _p(vc), _p(gate), gs[0], gs[1],
+                              _p(out), H * D, D, nthreads, int(bool(p16)))
     if r:
         raise ValueError("bn_or_attend rejected the shape")
     return out
 
 
-def decode_ragged(q, kc, vc, kv_off, kv_len, gate=None, chunk=0, nthreads=0):
+def decode_ragged(q, kc, vc, kv_off, kv_len, gate=None, chunk=0, nthreads=0, p16=False):
     nseq, H = q.shape[0], q.shape[1]
     KV = kc.shape[1]
     q = np.ascontiguousarray(q, np.float32)
@@ -132,8 +137,8 @@ def decode_ragged(q, kc, vc, kv_off, kv_len, gate=None, chunk=0, nthreads=0):
     kv_off = np.ascontiguousarray(kv_off, np.int64)
     kv_len = np.ascontiguousarray(kv_len, np.int32)
     out = np.empty((nseq, H, D), dtype=np.float32)
-    r = lib().bn_or_decode_ragged(nseq, H, KV, chunk, _p(q), H * D, _p(kc), _p(vc), _p(kv_off), _p(kv_len),
-                                  _p(gate), H * D, _p(out), H * D, nthreads)
+    r = lib().bn_or_decode_ragged_ex(nseq, H, KV, chunk, _p(q), H * D, _p(kc), _p(vc), _p(kv_off), _p(kv_len),
+                                     _p(gate), H * D, _p(out), H * D, nthreads, int(bool(p16)))
     if r:
         raise ValueError("bn_or_decode_ragged rejected the shape")
     return out

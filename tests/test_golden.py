@@ -70,12 +70,14 @@ def test_oracle_reproduces_golden_ragged(path):
     assert np.array_equal(out, g["out"])
 
 
-def _parity(out, ref, H):
+def _parity(out, ref, H, ref16):
     err = float(np.max(np.abs(out - ref)))
     assert err <= TOL, err
     R = workload.projection(H)
-    bad, _ = workload.argmax_mismatches(out, ref, R)
+    bad, ties = workload.argmax_mismatches(out, ref, R, ref16)
+    print(f"golden: max-abs {err:.3e}, {len(ties)} tie rows excused {ties.tolist()}", flush=True)
     assert len(bad) == 0
+    assert len(ties) <= workload.tie_cap(ref.shape[0])
 
 
 @pytest.mark.gpu
@@ -90,8 +92,8 @@ def test_hip_matches_golden(gpu, path):
     gate = t(g["gate"]) if "gate" in g else None
     out = ba.attention(ctx, ws, t(g["q"]), kc, vc, off, k_new=t(g["k_new"]), v_new=t(g["v_new"]), gate=gate)
     torch.cuda.synchronize()
-    _parity(out.cpu().numpy(), g["out"], H)
     kc_ref, vc_ref = cache_after(g, range(off, off + T))
+    _parity(out.cpu().numpy(), g["out"], H, oracle.attend(g["q"], kc_ref, vc_ref, off, g.get("gate"), p16=True))
     assert np.array_equal(kc.cpu().numpy().view(np.uint16), kc_ref)
     assert np.array_equal(vc.cpu().numpy().view(np.uint16), vc_ref)
 
@@ -108,7 +110,8 @@ def test_hip_matches_golden_ragged(gpu, path):
     out = ba.decode_ragged(ctx, ws, t(g["q"]), kc, vc, t(g["kv_off"]), t(g["kv_len"]), int(g["kv_len"].max()),
                            k_new=t(g["k_new"]), v_new=t(g["v_new"]), gate=t(g["gate"]))
     torch.cuda.synchronize()
-    _parity(out.cpu().numpy(), g["out"], H)
     kc_ref, vc_ref = cache_after(g, g["kv_off"] + g["kv_len"] - 1)
+    _parity(out.cpu().numpy(), g["out"], H,
+            oracle.decode_ragged(g["q"], kc_ref, vc_ref, g["kv_off"], g["kv_len"], g["gate"], p16=True))
     assert np.array_equal(kc.cpu().numpy().view(np.uint16), kc_ref)
     assert np.array_equal(vc.cpu().numpy().view(np.uint16), vc_ref)

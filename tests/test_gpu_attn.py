@@ -1,9 +1,10 @@
 """Parity of the HIP attention path (through the C ABI) with the oracle, on the GPU.
 
 Bar (from the task): outputs within max-abs 2e-3 of the oracle (fp32 accumulate), an identical argmax of
-each output row projected by a fixed random matrix (rows whose two best projected reference values tie within
-1e-4 relative are not compared: fp16 rounding alone can swap them), bit-exact fp16 cache rows after the
-append, and bit-identical results across repeated runs.
+each output row projected by a fixed random matrix (rows whose two best projected reference values lie within
+3 sqrt(2) |ref16 - ref| are ties, not compared, at most max(2, rows / 100) of them; ref16 is the oracle with
+fp16-rounded probabilities, so the margin does not depend on the output under test), bit-exact fp16 cache rows
+after the append, and bit-identical results across repeated runs.
 """
 import numpy as np
 import pytest
@@ -39,23 +40,28 @@ def cache_np(t):
     return t.cpu().numpy().view(np.uint16)
 
 
-def assert_parity(out, ref, H, what=""):
+def assert_parity(out, ref, H, what, ref16):
+    """max-abs within TOL and the projected argmax equal on every row that is not a tie; ties are sized by the
+    perturbed oracle ref16 (probabilities rounded to fp16), not by `out`, and printed."""
     err = float(np.max(np.abs(out - ref)))
     assert err <= TOL, f"{what} max-abs {err:.3e} > {TOL}"
     R = workload.projection(H)
-    bad, ties = workload.argmax_mismatches(out, ref, R)
+    bad, ties = workload.argmax_mismatches(out, ref, R, ref16)
+    rows = ref.shape[0]
+    print(f"{what}: max-abs {err:.3e}; argmax on {rows} rows, {len(ties)} tie rows excused {ties.tolist()[:32]}",
+          flush=True)
     assert len(bad) == 0, f"{what} projected argmax differs in rows {bad[:8]}"
-    # ties are rare (about 1% of rows with the error-scaled margin); many would mean the check lost its power
-    assert len(ties) <= max(4, out.shape[0] // 50), f"{what}: {len(ties)} tie rows"
+    assert len(ties) <= workload.tie_cap(rows), f"{what}: {len(ties)} tie rows"
     return err
 
 
 def check_case(gpu, inp, kind=ba.KIND_FORWARD, rows=None):
     out, d = run(gpu, inp, kind)
     ref, kc_ref, vc_ref = workload.expected(inp, rows=rows)
+    ref16, _, _ = workload.expected(inp, rows=rows, p16=True)
     T = inp["T"]
     got = out if rows is None else out[list(rows)]
-    err = assert_parity(got, ref, inp["H"], f"T={T} off={inp['off']}")
+    err = assert_parity(got, ref, inp["H"], f"T={T} off={inp['off']}", ref16)
     assert np.array_equal(cache_np(d["kc"]), kc_ref), "K cache differs after the append"
     assert np.array_equal(cache_np(d["vc"]), vc_ref), "V cache differs after the append"
     # repeat on the updated cache without the append: same bits
@@ -88,7 +94,7 @@ def test_decode_without_append_reads_cache_row(gpu):
     inp2 = dict(inp, kc=kc, vc=vc)
     out, _ = run(gpu, inp2, ba.KIND_DECODE, append=False)
     ref = oracle.attend(inp["q"], kc, vc, inp["off"], inp["gate"])
-    assert_parity(out, ref, 8)
+    assert_parity(out, ref, 8, "decode from the cache", oracle.attend(inp["q"], kc, vc, inp["off"], inp["gate"], p16=True))
 
 
 def test_gate_in_place_from_qproj(gpu):
@@ -101,7 +107,8 @@ def test_gate_in_place_from_qproj(gpu):
                        gate=qp_d[:, :, 256:], g_strides=(8 * 512, 512))
     torch.cuda.synchronize()
     ref, _, _ = workload.expected(dict(inp, gate=qp[:, :, 256:]))
-    assert_parity(out.cpu().numpy(), ref, 8)
+    ref16, _, _ = workload.expected(dict(inp, gate=qp[:, :, 256:]), p16=True)
+    assert_parity(out.cpu().numpy(), ref, 8, "gate from the q projection", ref16)
 
 
 def test_verify_8_workload(gpu):
@@ -217,12 +224,13 @@ def run_ragged(gpu, lens, offs, kc, vc, q, k_new, v_new, z):
         kc_ref[r] = k_new[i].astype(np.float16).view(np.uint16)
         vc_ref[r] = v_new[i].astype(np.float16).view(np.uint16)
     ref = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens, z)
+    ref16 = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens, z, p16=True)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     kc_d, vc_d = t(kc.view(np.int16)), t(vc.view(np.int16))
     out = ba.decode_ragged(ctx, ws, t(q), kc_d, vc_d, t(offs), t(lens), int(lens.max()), k_new=t(k_new),
                            v_new=t(v_new), gate=t(z))
     torch.cuda.synchronize()
-    assert_parity(out.cpu().numpy(), ref, H, "ragged")
+    assert_parity(out.cpu().numpy(), ref, H, "ragged", ref16)
     assert np.array_equal(cache_np(kc_d), kc_ref)
     assert np.array_equal(cache_np(vc_d), vc_ref)
 
@@ -240,13 +248,15 @@ def test_workspace_reused_across_shapes(gpu):
                            gate=d["gate"])
         torch.cuda.synchronize()
         ref, _, _ = workload.expected(inp)
-        assert_parity(out.cpu().numpy(), ref, H, f"reuse T={T} off={off}")
+        ref16, _, _ = workload.expected(inp, p16=True)
+        assert_parity(out.cpu().numpy(), ref, H, f"reuse T={T} off={off}", ref16)
     lens, offs, kc, vc, q, k_new, v_new, z = make_ragged(99, 32, 16, 4, 1024, 4096)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     out = ba.decode_ragged(ctx, ws, t(q), t(kc.view(np.int16)), t(vc.view(np.int16)), t(offs), t(lens),
                            int(lens.max()))
     torch.cuda.synchronize()
-    assert_parity(out.cpu().numpy(), oracle.decode_ragged(q, kc, vc, offs, lens), 16, "reuse ragged")
+    assert_parity(out.cpu().numpy(), oracle.decode_ragged(q, kc, vc, offs, lens), 16, "reuse ragged",
+                  oracle.decode_ragged(q, kc, vc, offs, lens, p16=True))
 
 
 def test_bad_arguments_do_not_launch(gpu):

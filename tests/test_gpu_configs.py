@@ -2,7 +2,8 @@
 
 The benchmarked workloads are drawn on the GPU by bench.py's own input functions (the same seeds and shapes), copied
 to the host, and every output row is compared with the oracle (max-abs 2e-3, projected argmax; rows whose two best
-projected reference values tie within 1e-4 relative are not compared). Cache rows written by the call are compared
+projected reference values tie within the margin that the oracle with fp16-rounded probabilities sets are not
+compared, at most max(2, rows / 100) of them). Cache rows written by the call are compared
 bit for bit.
   - decode_8k_batch32: 32 sequences x 8192 fp16 KV rows, 16 query / 4 kv heads, append + gate (the headline);
   - ragged_32: 32 sequences with lengths from random.Random(0xB0A5A104) in [1024, 32768] (sum 507,255);
@@ -45,7 +46,8 @@ def ragged_case(gpu, lens, seed):
     kc_ref[last] = oracle.f32_to_f16(k_new)
     vc_ref[last] = oracle.f32_to_f16(v_new)
     ref = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens_np, z)
-    err = assert_parity(host(out), ref, H, f"ragged {nseq} seqs")
+    ref16 = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens_np, z, p16=True)
+    err = assert_parity(host(out), ref, H, f"ragged {nseq} seqs", ref16)
     kc1, vc1 = cache_np(x["kc"]), cache_np(x["vc"])
     assert np.array_equal(kc1[last], kc_ref[last]) and np.array_equal(vc1[last], vc_ref[last]), "appended rows"
     # every other row is untouched: compare in slices to bound host memory
@@ -79,7 +81,8 @@ def prefill_4k_case(gpu, q_f16, ctx=None):
     oracle.append(host(x["k_new"]), host(x["v_new"]), kc0, vc0, off)
     q32 = host(x["q"].float())  # the q the kernel read, exactly
     ref = oracle.attend(q32, kc0, vc0, off, host(x["gate"]))
-    err = assert_parity(host(out), ref, H, "prefill_4k")
+    ref16 = oracle.attend(q32, kc0, vc0, off, host(x["gate"]), p16=True)
+    err = assert_parity(host(out), ref, H, "prefill_4k", ref16)
     assert np.array_equal(cache_np(x["kc"]), kc0) and np.array_equal(cache_np(x["vc"]), vc0)
     print(f"prefill_4k parity: max-abs {err:.3e}", flush=True)
 
@@ -131,7 +134,7 @@ def test_verify_peaky_scores(gpu, w, T, off, H, KV):
                        kind=ba.KIND_VERIFY)
     torch.cuda.synchronize()
     ref, _, _ = workload.expected(inp)
-    assert_parity(host(out), ref, H, f"verify w={w}")
+    assert_parity(host(out), ref, H, f"verify w={w}", workload.expected(inp, p16=True)[0])
     for t in range(T):
         o = ba.attention(ctx, ws, d["q"][t:t + 1], d["kc"], d["vc"], off + t, gate=d["gate"][t:t + 1],
                          kind=ba.KIND_DECODE)
@@ -164,6 +167,6 @@ def test_prefill_peaky_scores(gpu, w, T, off, H, KV, q16, path):
                        kind=ba.KIND_PREFILL)
     torch.cuda.synchronize()
     ref, _, _ = workload.expected(inp)
-    assert_parity(host(out), ref, H, f"prefill w={w}")
+    assert_parity(host(out), ref, H, f"prefill w={w}", workload.expected(inp, p16=True)[0])
     if path == "prefill":
         ctx.close()

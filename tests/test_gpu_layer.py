@@ -69,14 +69,16 @@ def check_layer(g, T, off, H, KV, rotate, seed, q16=False):
     assert np.array_equal(vc[rows], vc_ref[rows])
     attn_ref = oracle.attend(q_ref, kc_ref, vc_ref, off, inp["qp"][:, :, D:])
     ref = attn_ref.reshape(T, H * D)
+    ref16 = oracle.attend(q_ref, kc_ref, vc_ref, off, inp["qp"][:, :, D:], p16=True).reshape(T, H * D)
     if rotate:
         qp_inf = np.zeros((T, H, 512), np.float32)
         qp_inf[:, :, D:] = np.inf  # sigmoid = 1: rotate the already-gated rows
         ref = oracle.gate_rotate(ref, qp_inf.reshape(T, -1), signs)
+        ref16 = oracle.gate_rotate(ref16, qp_inf.reshape(T, -1), signs)
     err = float(np.max(np.abs(got.reshape(T, H * D) - ref)))
     assert err <= 2e-3, err
     R = oracle.normal(workload.PROJ_SEED, 0, (H * D, 128)).astype(np.float64)
-    bad, _ = workload.argmax_mismatches(got.reshape(T, -1), ref, R)
+    bad, _ = workload.argmax_mismatches(got.reshape(T, -1), ref, R, ref16)
     assert len(bad) == 0, f"projected argmax differs on rows {bad}"
 
 

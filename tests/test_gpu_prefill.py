@@ -46,11 +46,7 @@ def run_case(pf, inp, q16=False, dev=None, append=True):
     return out.cpu().numpy(), d
 
 
-# (T, off, H, KV, gate): single-tile q-tiles, tails, offsets that are not multiples of 32 (rows with no key in
-# the second half), head counts with KV not dividing 8, 1 and 2 key tiles per group
-SHAPES = [(2, 0, 4, 1, True), (31, 0, 8, 2, True), (32, 0, 4, 1, False), (33, 0, 4, 1, True),
-          (50, 20, 8, 2, True), (64, 64, 8, 2, True), (100, 37, 12, 3, True), (130, 500, 16, 4, False),
-          (257, 0, 8, 2, True), (256, 512, 8, 2, True), (96, 1000, 4, 1, True), (3, 2000, 8, 2, True)]
+SHAPES = workload.PREFILL_SHAPES
 
 
 def fp16_exact(inp):
@@ -61,13 +57,11 @@ def fp16_exact(inp):
 @pytest.mark.parametrize("q16", [True, False])
 @pytest.mark.parametrize("T,off,H,KV,gate", SHAPES)
 def test_prefill_kernel_shapes(pf, T, off, H, KV, gate, q16):
-    inp = workload.layer(6000 + 7 * T + off, T=T, off=off, H=H, KV=KV, gate=gate)
-    if q16:
-        fp16_exact(inp)
+    inp = workload.prefill_shape_input(T, off, H, KV, gate, q16)
     print(f"prefill shapes: T={T} off={off} H={H} KV={KV} fp16 q {q16}", flush=True)
     out, d = run_case(pf, inp, q16=q16)
     ref, kc_ref, vc_ref = workload.expected(inp)
-    assert_parity(out, ref, H, f"prefill T={T} off={off} H={H} q16={q16}")
+    assert_parity(out, ref, H, f"prefill T={T} off={off} H={H} q16={q16}", workload.expected(inp, p16=True)[0])
     assert np.array_equal(cache_np(d["kc"]), kc_ref)
     assert np.array_equal(cache_np(d["vc"]), vc_ref)
     out2, _ = run_case(pf, inp, q16=q16, dev=d, append=False)
@@ -79,7 +73,7 @@ def test_prefill_kernel_fp16_q(pf):
     inp["q"] = inp["q"].astype(np.float16).astype(np.float32)  # values the fp16 path carries exactly
     out, _ = run_case(pf, inp, q16=True)
     ref, _, _ = workload.expected(inp)
-    assert_parity(out, ref, 8, "prefill_kernel fp16 q")
+    assert_parity(out, ref, 8, "prefill_kernel fp16 q", workload.expected(inp, p16=True)[0])
 
 
 @pytest.mark.parametrize("q16", [True, False])
@@ -96,7 +90,7 @@ def test_prefill_kernel_rescale_on_late_dominant_key(pf, q16):
         fp16_exact(inp)  # 8 k_j is exact in fp16
     out, _ = run_case(pf, inp, q16=q16)
     ref, _, vc_ref = workload.expected(inp)
-    assert_parity(out, ref, 4, "prefill_kernel rescale")
+    assert_parity(out, ref, 4, "prefill_kernel rescale", workload.expected(inp, p16=True)[0])
     assert np.max(np.abs(out[50, 2] - oracle.f16_to_f32(vc_ref[250, 0]))) < 2e-3
     assert np.max(np.abs(out[60, 1] - oracle.f16_to_f32(vc_ref[290, 0]))) < 2e-3
 

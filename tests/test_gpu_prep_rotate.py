@@ -208,9 +208,11 @@ def test_layer_chain_matches_oracle(gpu, T, off):
     q_ref, kc_ref, vc_ref = oracle_prep(inp)
     attn_ref = oracle.attend(q_ref, kc_ref, vc_ref, off)
     ref = oracle.gate_rotate(attn_ref.reshape(T, W), inp["qp"].reshape(T, -1), signs)
+    attn16 = oracle.attend(q_ref, kc_ref, vc_ref, off, p16=True)
+    ref16 = oracle.gate_rotate(attn16.reshape(T, W), inp["qp"].reshape(T, -1), signs)
     out = xr.cpu().numpy()
     err = float(np.max(np.abs(out - ref)))
     assert err <= 2e-3, err
     R = oracle.normal(workload.PROJ_SEED, 0, (W, 128)).astype(np.float64)
-    bad, ties = workload.argmax_mismatches(out, ref, R)
+    bad, ties = workload.argmax_mismatches(out, ref, R, ref16)
     assert len(bad) == 0, f"projected argmax differs on rows {bad}"

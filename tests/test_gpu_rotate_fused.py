@@ -54,7 +54,9 @@ def check_rotated(g, inp, kind, q16=False):
     got = rot.reshape(T, H * D).cpu().numpy()
     assert float(np.max(np.abs(got - sep.cpu().numpy()))) <= 1e-6
     ref, _, _ = workload.expected(inp)
-    assert_parity(got.reshape(T, H, D), oracle_rotate(ref, signs).reshape(T, H, D), H, f"rotated T={T} off={off}")
+    ref16, _, _ = workload.expected(inp, p16=True)
+    assert_parity(got.reshape(T, H, D), oracle_rotate(ref, signs).reshape(T, H, D), H, f"rotated T={T} off={off}",
+                  oracle_rotate(ref16, signs).reshape(T, H, D))
 
 
 @pytest.mark.parametrize("L,H,KV", [(1, 8, 2), (64, 8, 2), (65, 8, 2), (5000, 8, 2), (3000, 16, 4)])
@@ -103,4 +105,6 @@ def test_ragged_rotated(gpu, nseq, lo, hi):
         kc_ref[r] = k_new[i].astype(np.float16).view(np.uint16)
         vc_ref[r] = v_new[i].astype(np.float16).view(np.uint16)
     ref = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens, z)
-    assert_parity(got.reshape(nseq, H, D), oracle_rotate(ref, signs).reshape(nseq, H, D), H, "ragged rotated")
+    ref16 = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens, z, p16=True)
+    assert_parity(got.reshape(nseq, H, D), oracle_rotate(ref, signs).reshape(nseq, H, D), H, "ragged rotated",
+                  oracle_rotate(ref16, signs).reshape(nseq, H, D))

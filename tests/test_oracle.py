@@ -19,8 +19,9 @@ import workload
 D = 256
 
 
-def brute(q, kc, vc, off, gate=None):
-    """float64 closed form: out[t,h] = softmax_j<off+t+1 (q.k_j / 16) . v_j, then * sigmoid(gate)."""
+def brute(q, kc, vc, off, gate=None, p16=False):
+    """float64 closed form: out[t,h] = softmax_j<off+t+1 (q.k_j / 16) . v_j, then * sigmoid(gate). p16: each
+    probability exp(s_j - max s) rounded to fp16 before both sums."""
     kf = oracle.f16_to_f32(kc).astype(np.float64)
     vf = oracle.f16_to_f32(vc).astype(np.float64)
     T, H = q.shape[0], q.shape[1]
@@ -31,6 +32,8 @@ def brute(q, kc, vc, off, gate=None):
             kh = h // 4
             s = kf[:n, kh, :] @ q[t, h].astype(np.float64) / 16.0
             p = np.exp(s - s.max())
+            if p16:
+                p = p.astype(np.float16).astype(np.float64)
             out[t, h] = (p @ vf[:n, kh, :]) / p.sum()
     if gate is not None:
         out = out / (1.0 + np.exp(-gate.astype(np.float64)))
@@ -296,6 +299,44 @@ def test_gate_rotate_is_scaled_sylvester_hadamard():
         x = attn[t].astype(np.float64) / (1.0 + np.exp(-g)) * signs
         ref = np.concatenate([Hm @ x[b:b + 512] for b in range(0, W, 512)])
         assert np.max(np.abs(xr[t] - ref)) < 2e-5
+
+
+def test_p16_oracle_is_fp16_probabilities():
+    """The perturbed oracle (the argmax tie margin's error budget) is the closed form with every probability
+    rounded to fp16, and it differs from the exact oracle by about the fp16 rounding of P: more than fp32 noise,
+    far less than the parity bar. One chunk covers every row's keys here, so the chunk max is the row max."""
+    inp = workload.layer(321, T=3, off=40, H=4, KV=1)
+    kc, vc = inp["kc"].copy(), inp["vc"].copy()
+    oracle.append(inp["k_new"], inp["v_new"], kc, vc, inp["off"])
+    exact = oracle.attend(inp["q"], kc, vc, 40, inp["gate"])
+    pert = oracle.attend(inp["q"], kc, vc, 40, inp["gate"], p16=True)
+    assert np.max(np.abs(pert - brute(inp["q"], kc, vc, 40, inp["gate"], p16=True))) < 2e-6
+    d = np.max(np.abs(pert - exact))
+    assert 1e-6 < d < 1e-3, d
+    # ragged decodes carry the flag too
+    offs, lens = np.array([0], np.int64), np.array([43], np.int32)
+    r16 = oracle.decode_ragged(inp["q"][2:3], kc, vc, offs, lens, inp["gate"][2:3], p16=True)
+    assert np.array_equal(r16[0], pert[2])
+
+
+def test_argmax_tie_margin_comes_from_the_perturbed_reference():
+    """With ref16 given, a reference row is a tie exactly when its top-2 projected gap is below
+    3 sqrt(2) |ref16 - ref| of that row (and above the 1e-4 relative floor); the output under test plays no part."""
+    rng = np.random.default_rng(5)
+    H, T = 4, 4
+    R = workload.projection(H)
+    ref = rng.standard_normal((T, H, 256)).astype(np.float32)
+    proj = ref.reshape(T, -1).astype(np.float64) @ R
+    gap = np.sort(proj, axis=1)[:, -1] - np.sort(proj, axis=1)[:, -2]
+    ref16 = ref.copy()
+    e = rng.standard_normal(H * 256)
+    e /= np.linalg.norm(e)
+    scale = gap / (workload.TIE_SIGMAS * np.sqrt(2.0))  # |e16| at which a row's gap equals its margin
+    for t, f in enumerate((2.0, 0.5, 1.2, 0.8)):  # rows 0 and 2: gap below the margin (ties); 1 and 3: above
+        ref16[t] = (ref[t].reshape(-1) + f * scale[t] * e).reshape(H, 256)
+    for out in (ref, ref + 1e-3 * rng.standard_normal(ref.shape).astype(np.float32)):
+        bad, ties = workload.argmax_mismatches(out, ref, R, ref16)
+        assert list(ties) == [0, 2] and len(bad) == 0
 
 
 def test_argmax_check_flags_flips_and_excuses_only_ties():

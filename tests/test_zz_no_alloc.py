@@ -23,9 +23,10 @@ def _batch(torch, seed, nseq, H, KV, lo, hi):
         kc_ref[r] = k_new[i].astype(np.float16).view(np.uint16)
         vc_ref[r] = v_new[i].astype(np.float16).view(np.uint16)
     ref = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens, z)
+    ref16 = oracle.decode_ragged(q, kc_ref, vc_ref, offs, lens, z, p16=True)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     dev = dict(q=t(q), offs=t(offs), lens=t(lens), k_new=t(k_new), v_new=t(v_new), z=t(z))
-    return lens, kc, vc, kc_ref, vc_ref, ref, dev
+    return lens, kc, vc, kc_ref, vc_ref, (ref, ref16), dev
 
 
 @pytest.mark.parametrize("first,second", [
@@ -47,7 +48,7 @@ def test_noalloc_matches_workspace_call(gpu, first, second):
         torch.cuda.synchronize()
         a, b = out_ws.cpu().numpy(), out_na.cpu().numpy()
         assert np.array_equal(a, b), f"noalloc differs from the workspace call by {np.max(np.abs(a - b)):.3e}"
-        assert_parity(b, ref, H, "noalloc")
+        assert_parity(b, ref[0], H, "noalloc", ref[1])
         assert np.array_equal(cache_np(kc_b), kc_ref) and np.array_equal(cache_np(vc_b), vc_ref)
         assert np.array_equal(cache_np(kc_a), kc_ref) and np.array_equal(cache_np(vc_a), vc_ref)
 
