@@ -437,7 +437,8 @@ def cpu_baseline(budget_s=8.0, H=16, KV=4, L=8192, nseq=4):
 
 
 ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix",
-       "decode_8k_batch32_rotated", "prefill_4k_rotated", "verify_8_rotated", "prep_4k", "prep_decode",
+       "decode_8k_batch32_rotated", "prefill_4k_rotated", "prefill_4k_f32q", "verify_8_rotated", "prep_4k",
+       "prep_decode",
        "gate_rotate_4k", "verify_8k_4b", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k", "kv_copy_8x4k",
        "qkv_decode_4b", "qkv_verify_8_4b", "qkv_prefill_4k_4b", "o_proj_decode_4b", "o_proj_prefill_4k_4b",
        "block_decode_8k_4b", "block_verify_8_4b", "block_prefill_4k_4b")
@@ -485,6 +486,7 @@ def main():
         log("prefill_4k")
         res["prefill_4k"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
                                        0xB0A5A103, q_f16=True)
+        r["steps"], r["warmup"] = max(2, K // 4), max(1, Wm // 2)
         log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
     if "ragged_32" in only:
         lens = ragged_lengths()
@@ -516,6 +518,11 @@ def main():
         log("prefill_4k_rotated")
         res["prefill_4k_rotated"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
                                                0xB0A5A103, q_f16=True, rotate=True)
+        log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
+    if "prefill_4k_f32q" in only:
+        log("prefill_4k_f32q (fp32 q: the reference's precision, fp16 hi/lo pair on prefill_hilo_kernel)")
+        res["prefill_4k_f32q"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
+                                            0xB0A5A103, q_f16=False)
         log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
     if "verify_8_rotated" in only:
         log("verify_8_rotated")
@@ -597,7 +604,8 @@ def main():
     pre = res.get("prefill_4k")
     if pre:
         line["prefill"] = {"workload": "prefill_4k", "value": round(pre["tflops"], 3), "unit": "TFLOP/s",
-                           "ms_per_step": round(pre["ms"], 5), "flops": pre["flops"], "peak": MFMA_F16_PEAK_TFLOPS,
+                           "ms_per_step": round(pre["ms"], 5), "steps": pre["steps"], "warmup": pre["warmup"],
+                           "flops": pre["flops"], "peak": MFMA_F16_PEAK_TFLOPS,
                            "frac": round(pre["tflops"] / MFMA_F16_PEAK_TFLOPS, 5)}
     others = {}
     for name in ALL[2:]:

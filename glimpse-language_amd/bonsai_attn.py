@@ -27,7 +27,7 @@ EXPORTS = (
     "bn_attn_append", "bn_attn_decode_ragged", "bn_prep_check", "bn_rotate_check", "bn_attn_prep",
     "bn_gate_rotate", "bn_attn_layer", "bn_layer_check", "bn_kv_copy", "bn_kv_section_size", "bn_kv_section_save",
     "bn_kv_section_check", "bn_kv_section_load", "bn_ternary_check", "bn_ternary_matmul", "bn_norm_check",
-    "bn_norm_rotate", "bn_attn_decode_ragged_noalloc", "bn_ternary_workspace_size",
+    "bn_norm_rotate", "bn_attn_decode_ragged_noalloc", "bn_ternary_workspace_size", "bn_dyn_overflow",
 )
 KV_SECTION_MAGIC = b"BNKVF16\0"
 KV_SECTION_HEADER = 24
@@ -145,6 +145,8 @@ def load(path=LIB_PATH):
     lib.bn_ctx_last_error.restype = ctypes.c_char_p
     lib.bn_abi_version.argtypes = []
     lib.bn_abi_version.restype = ctypes.c_int
+    lib.bn_dyn_overflow.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]
+    lib.bn_dyn_overflow.restype = ctypes.c_int
     lib.bn_attn_workspace_size.argtypes = [ctypes.POINTER(AttnArgs)]
     lib.bn_attn_workspace_size.restype = ctypes.c_size_t
     lib.bn_ragged_workspace_size.argtypes = [ctypes.POINTER(RaggedArgs)]
@@ -236,6 +238,13 @@ class Context:
 
     def error(self):
         return self.lib.bn_ctx_last_error(self.h).decode()
+
+    def dyn_overflow(self):
+        """Reads and clears the device's overflow flag (bn_dyn_overflow): True if a call since the last read found
+        a device offset above its host bound (it then attended as at the bound and appended nothing)."""
+        flag = ctypes.c_int(0)
+        self._check(self.lib.bn_dyn_overflow(self.h, ctypes.byref(flag)), "bn_dyn_overflow")
+        return bool(flag.value)
 
     def _stream(self, stream):
         if stream is not None:

@@ -9,6 +9,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <tuple>
+#include <utility>
 
 #include "bn_decode.h"
 #include "bn_flash.h"
@@ -43,6 +45,8 @@ struct bn_ctx {
     // this device's copy of `scratch` (the partials of bn_attn_decode_ragged_noalloc), or null if its address
     // could not be taken
     void* scratch;
+    // the first failed launch since the last status check (bn_launch's own return value), or hipSuccess
+    hipError_t launch_err;
     char err[256];
 };
 
@@ -138,9 +142,16 @@ DecodePlan plan_rows(const bn_attn_args* a, int64_t waves, int64_t target_waves,
     const bool exact = a->dyn == nullptr;
     DecodePlan p = plan_decode(T, a->KV, off + T, (T == 1 && exact) ? off + 1 : -1, waves, target_waves, max_splits);
     if (T > 1 && !exact) {
-        // the kernels' chunk is at least max(64, (off + T) / max_splits) keys for any device offset
+        // For any device offset d <= off the kernels' chunk is at least 64 keys, (off + T) / max_splits keys and
+        // sum / target keys, sum = T (d + 1) + T (T - 1) / 2 >= T (L - T + 1) the rows' keys (L = d + T, the longest
+        // row), so a row takes at most L target / (T (L - T + 1)) + 1 splits: at most 2 target / T + 1 when
+        // L >= 2T - 1, and at most ceil((2T - 2) / 64) by the 64-key floor below that.
         int64_t ns_max = ceil_div(off + T, bn::DEC_MIN_CHUNK);
         if (ns_max > max_splits) ns_max = max_splits;
+        int64_t by_target = 2 * p.target / T + 1;
+        const int64_t short_rows = ceil_div(2 * T - 2, bn::DEC_MIN_CHUNK);
+        if (by_target < short_rows) by_target = short_rows;
+        if (ns_max > by_target) ns_max = by_target;
         p.xcd_rows = true;
         p.units = 8 * T * ceil_div(ns_max, 8);
         p.slots = p.units;
@@ -347,8 +358,26 @@ void* scratch_address(int device) {
     return addr[device];
 }
 
+// Kernels are launched with hipLaunchKernel, whose return value is that launch's own status: the <<<>>> form
+// returns nothing, and the thread's sticky last error it leaves behind may also hold an error of other code on
+// the thread (which reading it would clear). The first failure since the last check is kept in the context.
+template <typename K, typename Vals, size_t... I>
+hipError_t launch_vals(K* kern, dim3 grid, dim3 block, size_t shm, hipStream_t st, Vals& vals,
+                       std::index_sequence<I...>) {
+    void* ptrs[] = {static_cast<void*>(&std::get<I>(vals))...};
+    return hipLaunchKernel(reinterpret_cast<const void*>(kern), grid, block, ptrs, shm, st);
+}
+template <typename... P, typename... A>
+void bn_launch(bn_ctx* ctx, void (*kern)(P...), dim3 grid, dim3 block, size_t shm, hipStream_t st, A&&... args) {
+    static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+    std::tuple<P...> vals(static_cast<P>(args)...);
+    const hipError_t e = launch_vals(kern, grid, block, shm, st, vals, std::index_sequence_for<P...>{});
+    if (e != hipSuccess && ctx->launch_err == hipSuccess) ctx->launch_err = e;
+}
+
 bn_status launched(bn_ctx* ctx, const char* what) {
-    hipError_t e = hipGetLastError();
+    const hipError_t e = ctx->launch_err;
+    ctx->launch_err = hipSuccess;
     if (e != hipSuccess) return set_err(ctx->err, BN_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
     return BN_OK;
 }
@@ -358,7 +387,7 @@ bn_status launch_append(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     const int64_t n8 = (int64_t)a->T * row / 8;
     int64_t blocks = ceil_div(n8, 256);
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(bn::append_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a->k_new, a->v_new, a->kc, a->vc,
+    bn_launch(ctx, bn::append_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a->k_new, a->v_new, a->kc, a->vc,
                        row, (int)a->off, a->dyn, n8);
     return launched(ctx, "append_kernel");
 }
@@ -366,19 +395,19 @@ bn_status launch_append(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
 bn_status launch_decode(bn_ctx* ctx, hipStream_t st, const bn::DecodeArgs& d, const DecodePlan& p) {
     const dim3 grid((unsigned)p.units, (unsigned)p.KV);
     switch (p.waves) {
-        case 1: hipLaunchKernelGGL(bn::decode_split_kernel<1>, grid, dim3(64), 0, st, d); break;
+        case 1: bn_launch(ctx, bn::decode_split_kernel<1>, grid, dim3(64), 0, st, d); break;
         case 2:
             if (p.xcd_rows)
-                hipLaunchKernelGGL((bn::decode_split_kernel<2, true>), grid, dim3(128), 0, st, d);
+                bn_launch(ctx, (bn::decode_split_kernel<2, true>), grid, dim3(128), 0, st, d);
             else
-                hipLaunchKernelGGL((bn::decode_split_kernel<2, false>), grid, dim3(128), 0, st, d);
+                bn_launch(ctx, (bn::decode_split_kernel<2, false>), grid, dim3(128), 0, st, d);
             break;
-        case 4: hipLaunchKernelGGL(bn::decode_split_kernel<4>, grid, dim3(256), 0, st, d); break;
-        default: hipLaunchKernelGGL(bn::decode_split_kernel<8>, grid, dim3(512), 0, st, d); break;
+        case 4: bn_launch(ctx, bn::decode_split_kernel<4>, grid, dim3(256), 0, st, d); break;
+        default: bn_launch(ctx, bn::decode_split_kernel<8>, grid, dim3(512), 0, st, d); break;
     }
     bn_status s = launched(ctx, "decode_split_kernel");
     if (s || !p.multi) return s;
-    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3((unsigned)p.nseq, (unsigned)(2 * p.KV)), dim3(512), 0, st, d);
+    bn_launch(ctx, bn::decode_combine_kernel, dim3((unsigned)p.nseq, (unsigned)(2 * p.KV)), dim3(512), 0, st, d);
     return launched(ctx, "decode_combine_kernel");
 }
 
@@ -488,10 +517,10 @@ bn_status run_verify(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int64_t
     v.chunk = (int)chunk;
     v.units = (int)units;
     if (v.q)
-        hipLaunchKernelGGL((bn::verify_kernel<BN_VERIFY_WAVES, true>), dim3((unsigned)ns, (unsigned)a->KV),
+        bn_launch(ctx, (bn::verify_kernel<BN_VERIFY_WAVES, true>), dim3((unsigned)ns, (unsigned)a->KV),
                            dim3(64 * BN_VERIFY_WAVES), 0, st, v);
     else
-        hipLaunchKernelGGL((bn::verify_kernel<BN_VERIFY_WAVES, false>), dim3((unsigned)ns, (unsigned)a->KV),
+        bn_launch(ctx, (bn::verify_kernel<BN_VERIFY_WAVES, false>), dim3((unsigned)ns, (unsigned)a->KV),
                            dim3(64 * BN_VERIFY_WAVES), 0, st, v);
     bn_status s = launched(ctx, "verify_kernel");
     if (s) return s;
@@ -517,7 +546,7 @@ bn_status run_verify(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int64_t
     d.xcd_rows = 1;
     d.chunk = (int)chunk;
     d.part = v.part;
-    hipLaunchKernelGGL(bn::decode_combine_kernel, dim3((unsigned)T, (unsigned)(2 * a->KV)), dim3(512), 0, st, d);
+    bn_launch(ctx, bn::decode_combine_kernel, dim3((unsigned)T, (unsigned)(2 * a->KV)), dim3(512), 0, st, d);
     return launched(ctx, "decode_combine_kernel");
 }
 
@@ -545,14 +574,14 @@ bn_status run_prefill(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     f.ntq = (int)ceil_div(a->T, bn::PF_BQ);
     const int64_t blocks = (int64_t)a->KV * f.ntq;
     if (f.q16 && ctx->prefill_pair) {
-        hipLaunchKernelGGL(bn::prefill_pair_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
+        bn_launch(ctx, bn::prefill_pair_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
         return launched(ctx, "prefill_pair_kernel");
     }
     if (f.q16) {
-        hipLaunchKernelGGL(bn::prefill_kernel, dim3((unsigned)blocks), dim3(512), 0, st, f);
+        bn_launch(ctx, bn::prefill_kernel, dim3((unsigned)blocks), dim3(512), 0, st, f);
         return launched(ctx, "prefill_kernel");
     }
-    hipLaunchKernelGGL(bn::prefill_hilo_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
+    bn_launch(ctx, bn::prefill_hilo_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
     return launched(ctx, "prefill_hilo_kernel");
 }
 
@@ -592,12 +621,12 @@ bn_status attend_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     }
     const int64_t blocks = (int64_t)a->KV * p.ntq * p.max_splits;
     if (f.q16)
-        hipLaunchKernelGGL((bn::flash_kernel<false>), dim3((unsigned)blocks), dim3(256), 0, st, f);
+        bn_launch(ctx, (bn::flash_kernel<false>), dim3((unsigned)blocks), dim3(256), 0, st, f);
     else
-        hipLaunchKernelGGL((bn::flash_kernel<true>), dim3((unsigned)blocks), dim3(256), 0, st, f);
+        bn_launch(ctx, (bn::flash_kernel<true>), dim3((unsigned)blocks), dim3(256), 0, st, f);
     bn_status s = launched(ctx, "flash_kernel");
     if (s || p.max_splits == 1) return s;
-    hipLaunchKernelGGL(bn::flash_combine_kernel, dim3(a->T, a->H), dim3(64), 0, st, f);
+    bn_launch(ctx, bn::flash_combine_kernel, dim3(a->T, a->H), dim3(64), 0, st, f);
     return launched(ctx, "flash_combine_kernel");
 }
 
@@ -614,7 +643,7 @@ bn_status rotate_in_place(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     r.x_hs = a->o_hs;
     r.T = (int)a->T;
     r.W = (int)a->H * bn::D;
-    hipLaunchKernelGGL(bn::rotate_kernel, dim3(a->T, a->H / 2), dim3(64), 0, st, r);
+    bn_launch(ctx, bn::rotate_kernel, dim3(a->T, a->H / 2), dim3(64), 0, st, r);
     return launched(ctx, "rotate_kernel");
 }
 
@@ -659,9 +688,9 @@ bn_status launch_prep(bn_ctx* ctx, hipStream_t st, const bn_prep_args* a, bool k
     // a few tokens (decode, verify): every 24 head rows of a token on a block of their own
     const int64_t rows = (kv_only ? 0 : a->H) + 2 * (int64_t)a->KV;
     if (a->T < 64)
-        hipLaunchKernelGGL((bn::prep_kernel<8, 3>), dim3(a->T, (unsigned)ceil_div(rows, 24)), dim3(512), 0, st, p);
+        bn_launch(ctx, (bn::prep_kernel<8, 3>), dim3(a->T, (unsigned)ceil_div(rows, 24)), dim3(512), 0, st, p);
     else
-        hipLaunchKernelGGL((bn::prep_kernel<4, 4>), dim3(a->T), dim3(256), 0, st, p);
+        bn_launch(ctx, (bn::prep_kernel<4, 4>), dim3(a->T), dim3(256), 0, st, p);
     return launched(ctx, "prep_kernel");
 }
 
@@ -822,19 +851,19 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
             case 1:
                 // long rows: two waves split each row group's words (half the serial passes per wave)
                 if (a->k >= BN_TERN_ROWS_SPLIT_K)
-                    hipLaunchKernelGGL((bn::tern_rows_kernel<1, 2>), dim3((unsigned)ceil_div(rows, 2 * bn::TERN_ROWS_WAVE)),
+                    bn_launch(ctx, (bn::tern_rows_kernel<1, 2>), dim3((unsigned)ceil_div(rows, 2 * bn::TERN_ROWS_WAVE)),
                                        dim3(256), 0, st, t);
                 else
-                    hipLaunchKernelGGL(bn::tern_rows_kernel<1>, grid, dim3(256), 0, st, t);
+                    bn_launch(ctx, bn::tern_rows_kernel<1>, grid, dim3(256), 0, st, t);
                 break;
-            case 2: hipLaunchKernelGGL(bn::tern_rows_kernel<2>, grid, dim3(256), 0, st, t); break;
-            case 3: hipLaunchKernelGGL(bn::tern_rows_kernel<3>, grid, dim3(256), 0, st, t); break;
-            case 4: hipLaunchKernelGGL(bn::tern_rows_kernel<4>, grid, dim3(256), 0, st, t); break;
+            case 2: bn_launch(ctx, bn::tern_rows_kernel<2>, grid, dim3(256), 0, st, t); break;
+            case 3: bn_launch(ctx, bn::tern_rows_kernel<3>, grid, dim3(256), 0, st, t); break;
+            case 4: bn_launch(ctx, bn::tern_rows_kernel<4>, grid, dim3(256), 0, st, t); break;
 #if BN_TERN_ROWS_MAX_T > 4
-            case 5: hipLaunchKernelGGL(bn::tern_rows_kernel<5>, grid, dim3(256), 0, st, t); break;
-            case 6: hipLaunchKernelGGL(bn::tern_rows_kernel<6>, grid, dim3(256), 0, st, t); break;
-            case 7: hipLaunchKernelGGL(bn::tern_rows_kernel<7>, grid, dim3(256), 0, st, t); break;
-            default: hipLaunchKernelGGL(bn::tern_rows_kernel<8>, grid, dim3(256), 0, st, t); break;
+            case 5: bn_launch(ctx, bn::tern_rows_kernel<5>, grid, dim3(256), 0, st, t); break;
+            case 6: bn_launch(ctx, bn::tern_rows_kernel<6>, grid, dim3(256), 0, st, t); break;
+            case 7: bn_launch(ctx, bn::tern_rows_kernel<7>, grid, dim3(256), 0, st, t); break;
+            default: bn_launch(ctx, bn::tern_rows_kernel<8>, grid, dim3(256), 0, st, t); break;
 #endif
         }
         return launched(ctx, "tern_rows_kernel");
@@ -845,11 +874,11 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
         const dim3 grid((unsigned)row_tiles);
         // fewer 64-row tiles than CUs (o_proj-sized matrices): 8 waves per block split K further
         if (row_tiles < ctx->cus && a->k % (8 * bn::TERN_KC) == 0)
-            hipLaunchKernelGGL((bn::tern_mfma_kernel<1, 8, 1>), grid, dim3(512), 0, st, t, row_tiles);
+            bn_launch(ctx, (bn::tern_mfma_kernel<1, 8, 1>), grid, dim3(512), 0, st, t, row_tiles);
         else if (tern_ksplit(a->k) == 4)
-            hipLaunchKernelGGL((bn::tern_mfma_kernel<1, 4, 1>), grid, dim3(256), 0, st, t, row_tiles);
+            bn_launch(ctx, (bn::tern_mfma_kernel<1, 4, 1>), grid, dim3(256), 0, st, t, row_tiles);
         else
-            hipLaunchKernelGGL((bn::tern_mfma_kernel<1, 2, 1>), grid, dim3(128), 0, st, t, row_tiles);
+            bn_launch(ctx, (bn::tern_mfma_kernel<1, 2, 1>), grid, dim3(128), 0, st, t, row_tiles);
         return launched(ctx, "tern_mfma_kernel<1>");
     }
     bool split_once = a->work != nullptr && bn::tern_pf_tiles((int)a->T, (int)a->k) <= (size_t)INT32_MAX;
@@ -858,7 +887,7 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
         // x split once into the workspace, then the GEMM streams it
         const size_t tiles = bn::tern_pf_tiles((int)a->T, (int)a->k);
         uint8_t* work = static_cast<uint8_t*>(a->work);
-        hipLaunchKernelGGL(bn::tern_split_kernel, dim3((unsigned)tiles), dim3(256), 0, st, a->x, a->x_ts, (int)a->T,
+        bn_launch(ctx, bn::tern_split_kernel, dim3((unsigned)tiles), dim3(256), 0, st, a->x, a->x_ts, (int)a->T,
                            (int)a->k, work);
         const int row_tiles = (int)ceil_div(rows, 256);
         const int64_t blocks = (int64_t)row_tiles * ceil_div(a->T, bn::TPF_BM);
@@ -866,10 +895,10 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
         // a grid that fits three blocks per CU in one round takes the 2-stage form (three blocks per CU); a larger
         // one the 3-stage form (two per CU, copies two chunks ahead)
         if (blocks <= 3 * (int64_t)ctx->cus)
-            hipLaunchKernelGGL((bn::tern_pf_kernel<2, 3>), dim3((unsigned)blocks), dim3(256), 0, st, t, row_tiles,
+            bn_launch(ctx, (bn::tern_pf_kernel<2, 3>), dim3((unsigned)blocks), dim3(256), 0, st, t, row_tiles,
                                (const uint8_t*)work);
         else
-            hipLaunchKernelGGL((bn::tern_pf_kernel<3, 2>), dim3((unsigned)blocks), dim3(256), 0, st, t, row_tiles,
+            bn_launch(ctx, (bn::tern_pf_kernel<3, 2>), dim3((unsigned)blocks), dim3(256), 0, st, t, row_tiles,
                                (const uint8_t*)work);
         return launched(ctx, "tern_pf_kernel");
     }
@@ -878,7 +907,7 @@ bn_status run_ternary(bn_ctx* ctx, hipStream_t st, const bn_ternary_args* a) {
     const int row_tiles = (int)ceil_div(rows, 64 * RG);
     const int64_t blocks = (int64_t)row_tiles * ceil_div(a->T, 32 * MT);
     if (blocks > INT32_MAX) return set_err(ctx->err, BN_EINVAL, "T * rows too large for one launch");
-    hipLaunchKernelGGL((bn::tern_mfma_kernel<MT, 1, RG, BN_TERN_PF_OCC, BN_TERN_PF_KC>), dim3((unsigned)blocks),
+    bn_launch(ctx, (bn::tern_mfma_kernel<MT, 1, RG, BN_TERN_PF_OCC, BN_TERN_PF_KC>), dim3((unsigned)blocks),
                        dim3(64 * RG), 0, st, t, row_tiles);
     return launched(ctx, "tern_mfma_kernel (prefill)");
 }
@@ -897,7 +926,7 @@ bn_status launch_lora(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     l.o_hs = a->o_hs;
     l.signs = a->signs;
     l.W = (int)a->H * bn::D;
-    hipLaunchKernelGGL(bn::lora_kernel, dim3(a->T, (unsigned)ceil_div(a->lora_r, l.l.rpb)), dim3(256),
+    bn_launch(ctx, bn::lora_kernel, dim3(a->T, (unsigned)ceil_div(a->lora_r, l.l.rpb)), dim3(256),
                        (size_t)l.W * sizeof(float), st, l);
     return launched(ctx, "lora_kernel");
 }
@@ -947,6 +976,22 @@ bn_status run_ragged(bn_ctx* ctx, hipStream_t st, const bn_ragged_args* a, const
 extern "C" {
 
 int bn_abi_version(void) { return BN_ABI_VERSION; }
+
+bn_status bn_dyn_overflow(bn_ctx* ctx, int* flag) {
+    if (!ctx || !flag) return BN_EINVAL;
+    int prev = -1;
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (hipSetDevice(ctx->device) != hipSuccess) return set_err(ctx->err, BN_EDEVICE, "hipSetDevice failed");
+    unsigned int v = 0;
+    const unsigned int zero = 0;
+    hipError_t e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(bn::dyn_overflow), sizeof(v), 0, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && v) e = hipMemcpyToSymbol(HIP_SYMBOL(bn::dyn_overflow), &zero, sizeof(zero), 0,
+                                                    hipMemcpyHostToDevice);
+    if (prev >= 0 && prev != ctx->device) (void)hipSetDevice(prev);
+    if (e != hipSuccess) return set_err(ctx->err, BN_EDEVICE, "dyn overflow flag: %s", hipGetErrorString(e));
+    *flag = v != 0;
+    return BN_OK;
+}
 
 const char* bn_status_str(bn_status s) {
     switch (s) {
@@ -1001,6 +1046,7 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
     c->prefill_pair = 0;
     if (const char* e = getenv("BONSAI_ATTN_PREFILL_PAIR")) c->prefill_pair = atoi(e) != 0;
     c->scratch = scratch_address(device);
+    c->launch_err = hipSuccess;
     c->err[0] = 0;
     *out = c;
     return BN_OK;
@@ -1037,7 +1083,7 @@ bn_status bn_workspace_clear(bn_ctx* ctx, bn_stream stream, void* ws, size_t byt
     int ntail = (int)(bytes % 16);
     int64_t blocks = ceil_div(n16 > 0 ? n16 : 1, 256);
     if (blocks > 2048) blocks = 2048;
-    hipLaunchKernelGGL(bn::fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+    bn_launch(ctx, bn::fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                        static_cast<bn::u4*>(ws), n16, static_cast<uint8_t*>(ws) + n16 * 16, ntail);
     return launched(ctx, "fill_zero_kernel");
 }
@@ -1283,11 +1329,11 @@ bn_status bn_norm_rotate(bn_ctx* ctx, bn_stream stream, const bn_norm_args* a) {
         n.lora.R = (int)a->lora_r;
         n.lora.rpb = waves * (a->T >= 64 ? 4 : 1);
         const unsigned extra = a->lora_r ? (unsigned)ceil_div(a->lora_r, n.lora.rpb) : 0u;
-        hipLaunchKernelGGL(bn::norm_rotate_row_kernel, dim3(a->T, 1 + extra), dim3(64 * waves),
+        bn_launch(ctx, bn::norm_rotate_row_kernel, dim3(a->T, 1 + extra), dim3(64 * waves),
                            a->lora_r ? (size_t)a->d * sizeof(float) : 0, (hipStream_t)stream, n);
         return launched(ctx, "norm_rotate_row_kernel");
     }
-    hipLaunchKernelGGL(bn::norm_rotate_kernel, dim3(a->T, a->d / 512), dim3(64), 0, (hipStream_t)stream, n);
+    bn_launch(ctx, bn::norm_rotate_kernel, dim3(a->T, a->d / 512), dim3(64), 0, (hipStream_t)stream, n);
     return launched(ctx, "norm_rotate_kernel");
 }
 
@@ -1322,7 +1368,7 @@ bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a)
     r.lora.R = (int)a->lora_r;
     r.lora.rpb = a->T >= 64 ? 16 : 4;
     const unsigned extra = a->lora_r ? (unsigned)ceil_div(a->lora_r, r.lora.rpb) : 0u;
-    hipLaunchKernelGGL(bn::rotate_kernel, dim3(a->T, a->H / 2 + extra), dim3(64),
+    bn_launch(ctx, bn::rotate_kernel, dim3(a->T, a->H / 2 + extra), dim3(64),
                        a->lora_r ? (size_t)r.W * sizeof(float) : 0, (hipStream_t)stream, r);
     return launched(ctx, "rotate_kernel");
 }

@@ -3,16 +3,19 @@
 // Semantics follow attn_split.comp:9-58 + attn_combine.comp:6-21 + gate_rotate.comp:19-22 of the reference
 // (query row of head h attends to cache rows [0, L) of kv head h/4, softmax(q.k / 16), gate a*sigmoid(z));
 // the decomposition is this kernel's own:
-//   grid (unit, kv head) x one wave. A split covers `chunk` consecutive keys of one sequence and one kv head
-//   and serves the 4 query heads that share it, so every K/V byte is read once.
-//   Balanced splits: the chunk follows the batch's total length, chunk = ceil(sum_i L_i / target) (rounded up
-//   to 16 keys, at least 64, at most the longest sequence), so a ragged batch gets about `target` equal splits
-//   per kv head however its lengths are spread. Sequence i takes n_i = ceil(L_i / chunk) consecutive units
-//   starting at P_i = sum_{k<i} n_k; every block derives chunk, P and n from the lengths itself (a wave-wide
-//   scan over the length array, which sits in L2), so there is no planning launch and a captured graph can
-//   be replayed with new device-side lengths. sum_i n_i <= target + nseq bounds the launch; units past the
-//   last split exit at once. The split structure is a function of the lengths only, so results are
-//   reproducible bit for bit.
+//   grid (unit, kv head) x W waves. A unit serves the 4 query heads that share its kv head, so every K/V byte is
+//   read once.
+//   Flat order (a batch of sequences): per kv head the keys of all sequences, in order, form one stream of
+//   sum_i L_i keys, cut into units of `chunk` keys, chunk ~ ceil(sum_i L_i / target) (a multiple of 16, at least
+//   64 and max_len / max_splits). A unit may hold the tail of one sequence, whole sequences and the head of the
+//   next (one segment each), so every unit but the last holds exactly `chunk` keys and the blocks are balanced
+//   however the lengths are spread; ceil(sum_i L_i / chunk) <= target bounds the launch, and units past the last
+//   exit at once. Segment (unit b, sequence i) writes partial-record slot b + i, so sequence i's records are
+//   contiguous. xcd_rows (the T rows of one call): each row takes ceil(L_t / chunk) splits of its own, placed so
+//   that a row's splits run on different XCDs (dec_slot). Every block derives chunk and its segments from the
+//   lengths itself (a wave-wide scan over the length array, which sits in L2), so there is no planning launch and
+//   a captured graph can be replayed with new device-side lengths. The split structure is a function of the
+//   lengths only, so results are reproducible bit for bit.
 //   QK^T: v_mfma_f32_16x16x32_f16 computes S^T = K Q^T over 16-key tiles. The A operand is the K tile read
 //   straight from HBM in MFMA layout (lane: key l%16, 8 dims per k-step); the B operand holds the 4 heads'
 //   query rows as an fp16 hi/lo pair (columns h and h+4, repeated in 8..15), so hi + lo carries the fp32
@@ -305,7 +308,8 @@ __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
         const int nt = (sj1 - sj0 + 15) >> 4;
         const int j0 = sj0 + 16 * (wave * nt / W);
         const int j1 = min(sj1, sj0 + 16 * ((wave + 1) * nt / W));
-        const bool has_new = a.k_new != nullptr && j1 == L && j0 < j1;  // this wave owns the appended row L-1
+        // this wave owns the appended row L-1 (none when a device offset lies past the bound: the flag is set)
+        const bool has_new = a.k_new != nullptr && j1 == L && j0 < j1 && !(a.dyn && dyn_over(a.dyn, a.len0 - 1));
         const int tl = j0 + (j1 - j0 - 1) / 16 * 16;          // first key of the wave's last (maybe partial) tile
         const int64_t kvd = (int64_t)a.KV * D;
         const uint16_t* kb = a.kc + (row0 * a.KV + kh) * D;

@@ -55,10 +55,23 @@ __device__ __forceinline__ float sum_xhalf(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// The cache offset of a call: the host value, or (graph replay) the device value at dyn, clamped to the host value,
-// which sizes the launch.
+// Set (to 1) by any kernel that finds a device offset above its call's host bound; kernels never clear it. The host
+// reads and clears it with bn_dyn_overflow. One copy per device, from the library's load until the process ends.
+__device__ unsigned int dyn_overflow;
+
+// The device offset at dyn lies above the host bound off_max: the call's cache appends are skipped.
+__device__ __forceinline__ bool dyn_over(const uint32_t* dyn, int off_max) {
+    return dyn != nullptr && *dyn > (uint32_t)off_max;
+}
+
+// The cache offset of a call: the host value, or (graph replay) the device value at dyn. A device value above the
+// host value (which sizes the launch) is taken as the host value, and the overflow flag is set (a vector atomic).
 __device__ __forceinline__ int call_off(const uint32_t* dyn, int off_max) {
-    return dyn ? (int)min(*dyn, (uint32_t)off_max) : off_max;
+    if (!dyn) return off_max;
+    const uint32_t d = *dyn;
+    if (d <= (uint32_t)off_max) return (int)d;
+    __hip_atomic_fetch_or(&dyn_overflow, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return off_max;
 }
 
 // reference gate: a * (1 / (1 + exp(-z)))  (gate_rotate.comp:19-22)

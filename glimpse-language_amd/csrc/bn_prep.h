@@ -96,11 +96,11 @@ struct PrepArgs {
 // 4l .. 4l+3 (x, already loaded; w the norm weights of those dims, cs/sn the token's rotation). q and k: norm
 // and rotation (norm_rope); v: copied. k and v are rounded to fp16 (nearest even) into cache row off + t.
 __device__ __forceinline__ void prep_row(const PrepArgs& a, int off, int t, int hh, f4 x, f4 w, f4 cs, f4 sn,
-                                         int lane) {
+                                         int lane, bool store_kv) {
     const int H = a.H, KV = a.KV, d0 = 4 * lane;
     if (hh >= H + KV) {
         const h4 y = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
-        *reinterpret_cast<h4*>(a.vc + ((int64_t)(off + t) * KV + (hh - H - KV)) * D + d0) = y;
+        if (store_kv) *reinterpret_cast<h4*>(a.vc + ((int64_t)(off + t) * KV + (hh - H - KV)) * D + d0) = y;
         return;
     }
     x = norm_rope(x, w, cs, sn, a.rp.rot, lane);
@@ -111,7 +111,7 @@ __device__ __forceinline__ void prep_row(const PrepArgs& a, int off, int t, int 
         } else {
             *reinterpret_cast<f4*>(a.q + t * a.q_ts + hh * a.q_hs + d0) = x;
         }
-    } else {
+    } else if (store_kv) {
         const h4 y = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
         *reinterpret_cast<h4*>(a.kc + ((int64_t)(off + t) * KV + (hh - H)) * D + d0) = y;
     }
@@ -130,6 +130,7 @@ __global__ __launch_bounds__(64 * PW) void prep_kernel(PrepArgs a) {
     const int H = a.H, KV = a.KV, nh = H + 2 * KV, d0 = 4 * lane;
     const int h_first = (a.q || a.q16) ? 0 : H;
     const int off = call_off(a.dyn, a.off);
+    const bool store_kv = !dyn_over(a.dyn, a.off);  // past the bound no K/V row is written (the flag is set)
     const int64_t kvd = (int64_t)KV * D;
     constexpr int R = PW * PB;
     auto load = [&](int h0, f4* x) {
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(64 * PW) void prep_kernel(PrepArgs a) {
 #pragma unroll
         for (int b = 0; b < PB; b++) {
             const int hh = h0 + PW * b;
-            if (hh < nh) prep_row(a, off, t, hh, x[b], hh < H ? wq : wk, cs, sn, lane);
+            if (hh < nh) prep_row(a, off, t, hh, x[b], hh < H ? wq : wk, cs, sn, lane, store_kv);
         }
     }
 }

@@ -11,6 +11,7 @@ __global__ __launch_bounds__(256) void append_kernel(const float* __restrict__ k
                                                      int64_t row, int off_max, const uint32_t* dyn, int64_t n8) {
     asm volatile("" ::"s"(kn), "s"(vn), "s"(kc), "s"(vc), "s"(row), "s"(n8));  // argument words in one round trip
     const int64_t o = (int64_t)call_off(dyn, off_max) * row;
+    if (dyn_over(dyn, off_max)) return;  // an offset past the bound appends nothing (the flag is set)
     uint16_t* kdst = kc + o;
     uint16_t* vdst = vc + o;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;

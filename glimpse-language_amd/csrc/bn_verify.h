@@ -106,7 +106,7 @@ __global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
 
     // The call's new rows [off, off + T) that fall in this wave's tiles go to the cache first (fp16, nearest even),
     // before the wave's copies read them: no other wave or block reads those rows (the tiles partition the keys).
-    if (a.k_new) {
+    if (a.k_new && !dyn_over(a.dyn, a.off)) {  // past the bound nothing is appended (the flag is set)
         const int r0 = max(off, k0 + j_begin * PF_BK), r1 = min(nk, k0 + j_end * PF_BK);
         if (r0 < r1) {
             f4 kn[8], vn[8];

@@ -11,7 +11,7 @@
 use std::ffi::{c_char, c_int, c_void, CStr};
 
 pub const BN_HEAD_DIM: u32 = 256;
-pub const BN_ABI_VERSION: c_int = 5;
+pub const BN_ABI_VERSION: c_int = 6;
 pub const BN_Q_F16: u32 = 1;
 pub const BN_NOALLOC_SCRATCH_BYTES: u32 = 16 << 20;
 pub const BN_KV_SECTION_MAGIC: &[u8; 8] = b"BNKVF16\0";
@@ -233,6 +233,7 @@ extern "C" {
     pub fn bn_status_str(s: bn_status) -> *const c_char;
     pub fn bn_ctx_last_error(ctx: *const bn_ctx) -> *const c_char;
     pub fn bn_abi_version() -> c_int;
+    pub fn bn_dyn_overflow(ctx: *mut bn_ctx, flag: *mut c_int) -> bn_status;
 
     pub fn bn_attn_workspace_size(a: *const bn_attn_args) -> usize;
     pub fn bn_ragged_workspace_size(a: *const bn_ragged_args) -> usize;

@@ -41,7 +41,7 @@ extern "C" {
 #endif
 
 #define BN_HEAD_DIM 256
-#define BN_ABI_VERSION 5
+#define BN_ABI_VERSION 6
 
 typedef enum bn_status {
     BN_OK = 0,
@@ -97,9 +97,10 @@ typedef struct bn_attn_args {
                             filled per step by gpu_vk.rs:1035-1049). The kernels read dyn[0] when they run and use
                             it in place of `off` (the rows' positions, the keys they see, the cache rows written);
                             `off` is then the largest offset the call may see, and sizes the launch and the
-                            workspace (a device value above it is taken as `off`). A call captured in a HIP graph
-                            thus replays at any offset up to `off`: the caller advances dyn[0] on the device
-                            between replays. */
+                            workspace. A call captured in a HIP graph thus replays at any offset up to `off`: the
+                            caller advances dyn[0] on the device between replays. A device value above `off` is an
+                            error the kernels cannot return: they attend as if it were `off`, append no row (the
+                            cache is left as it was), and set the device's overflow flag (bn_dyn_overflow). */
 
     /* LoRA down projection of the gated output (the extra rows gate_rotate computes, gate_rotate.comp:14,
      * rot.glsl:19-40, sized by rot_lora model.rs:444-454): u[t][r] = sum_e A[r][e] y[t][e], with y the gated
@@ -268,6 +269,11 @@ const char* bn_status_str(bn_status s);
 /* Text of the last failed check or launch on this context (empty if none). */
 const char* bn_ctx_last_error(const bn_ctx* ctx);
 int bn_abi_version(void);
+/* Reads and clears this context's device's overflow flag: *flag = 1 if any call since the last read found a device
+ * offset (dyn[0]) above its host bound `off` (the call then attended as at `off` and appended nothing), else 0.
+ * No counterpart in the reference (a Vulkan dispatch past its bound is undefined there). Synchronous: call it
+ * after the stream work that read the offsets has finished. Calls on one device share the flag. */
+bn_status bn_dyn_overflow(bn_ctx* ctx, int* flag);
 
 /* ---- sizes and checks (pure host code, no device access) ----------------------------------------- */
 size_t bn_attn_workspace_size(const bn_attn_args* a);

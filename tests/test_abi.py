@@ -34,7 +34,7 @@ def test_header_and_binding_agree():
 def test_library_exports_every_declared_symbol(lib):
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.bn_abi_version() == 5
+    assert lib.bn_abi_version() == 6
 
 
 def test_status_strings(lib):
@@ -111,6 +111,24 @@ def test_workspace_sizes(lib):
     assert sz > 0 and sz % 16 == 0
     # partial records of (m[4], l[4], acc[4][256]) floats per (sequence, kv head, split)
     assert sz % (4 * (8 + 4 * 256)) == 0
+
+
+@pytest.mark.parametrize("T,H,KV,bound", [(8, 16, 4, 32768), (8, 16, 4, 131072), (12, 8, 2, 32768),
+                                          (16, 16, 4, 131072), (2, 8, 2, 9000)])
+def test_device_offset_workspace_stays_near_the_exact_one(lib, T, H, KV, bound):
+    """With a device offset, `off` only bounds the rows' positions, and the workspace must cover every split count
+    the kernels derive from a smaller offset. The kernels' chunk grows with the rows' total length, so that count
+    stays near the exact one: the workspace is a small factor of the call at the bound without a device offset,
+    not a linear function of the bound."""
+    exact = good_args(T=T, off=bound - T, H=H, KV=KV)
+    dyn = good_args(T=T, off=bound - T, H=H, KV=KV)
+    dyn.dyn = 0x200000
+    w_exact, w_dyn = ba.workspace_size(exact), ba.workspace_size(dyn)
+    # the smallest offsets (a few keys per row) are covered too
+    w_small = ba.workspace_size(good_args(T=T, off=0, H=H, KV=KV))
+    assert w_dyn >= max(w_exact, w_small)
+    assert w_dyn <= 4 * max(w_exact, 1 << 20), (w_dyn, w_exact)
+
 
 
 def test_ragged_check(lib):

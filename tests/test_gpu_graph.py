@@ -137,6 +137,62 @@ def test_device_offset_every_path(gpu, T, off, off_max, H, KV, kind, min_blocks,
         ctx.close()
 
 
+# (T, off_max, H, KV, kind, min prefill blocks): a device offset past the host bound on every path that appends
+# (decode, verify rows, the append kernel before a prefill, the prefill kernels)
+@pytest.mark.parametrize("T,off_max,H,KV,kind,min_blocks", [
+    (1, 3000, 16, 4, ba.KIND_DECODE, 0),
+    (8, 2048, 8, 2, ba.KIND_VERIFY, 0),
+    (100, 300, 8, 2, ba.KIND_PREFILL, 0),
+    (64, 200, 8, 2, ba.KIND_PREFILL, 1),
+])
+def test_device_offset_past_the_bound_is_flagged_and_appends_nothing(gpu, T, off_max, H, KV, kind, min_blocks):
+    """dyn[0] above `off` cannot be returned as an error by the kernels: they attend as at `off`, write no cache
+    row and set the device's overflow flag, which bn_dyn_overflow reads and clears. A call within the bound after it
+    leaves the flag clear."""
+    torch = gpu[0]
+    if min_blocks:
+        ctx = context_with(BONSAI_ATTN_PREFILL_MIN_BLOCKS=min_blocks)
+        ws = ba.Workspace(ctx, "cuda")
+    else:
+        _, ctx, ws = gpu
+    assert ctx.dyn_overflow() in (False, True)  # clears what earlier tests left
+    inp = workload.layer(0x6E00 + T + off_max, T=T, off=off_max, H=H, KV=KV, cap=off_max + T)
+    print(f"device offset past the bound: T={T} bound {off_max} dyn {off_max + 7} kind {kind}", flush=True)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    kc, vc = t(inp["kc"].view(np.int16)), t(inp["vc"].view(np.int16))
+    dyn = torch.tensor([off_max + 7], dtype=torch.int32, device="cuda")
+    out = ba.attention(ctx, ws, t(inp["q"]), kc, vc, off_max, k_new=t(inp["k_new"]), v_new=t(inp["v_new"]),
+                       gate=t(inp["gate"]), kind=kind, dyn=dyn)
+    torch.cuda.synchronize()
+    assert ctx.dyn_overflow() is True
+    assert ctx.dyn_overflow() is False  # read and cleared
+    assert np.array_equal(cache_np(kc), inp["kc"]) and np.array_equal(cache_np(vc), inp["vc"]), "cache rows changed"
+    assert np.all(np.isfinite(out.cpu().numpy()))
+    dyn.fill_(off_max - 3 if T == 1 else 0)
+    ba.attention(ctx, ws, t(inp["q"]), kc, vc, off_max, k_new=t(inp["k_new"]), v_new=t(inp["v_new"]),
+                 gate=t(inp["gate"]), kind=kind, dyn=dyn)
+    torch.cuda.synchronize()
+    assert ctx.dyn_overflow() is False
+    if min_blocks:
+        ctx.close()
+
+
+def test_layer_device_offset_past_the_bound_appends_nothing(gpu):
+    """The one-call layer with dyn[0] past the bound: prep_kernel writes no K/V row and the flag is set."""
+    torch, ctx, ws = gpu
+    T, off_max, H, KV = 8, 2000, 8, 2
+    ctx.dyn_overflow()
+    inp = prep_inputs(0x6F00, T, off_max, H, KV)
+    print("layer device offset past the bound: T=8 bound 2000 dyn 2009", flush=True)
+    dev = {k: to_dev(torch, inp[k]) for k in ("qp", "kp", "vp", "qn", "kn", "pos", "inv", "kc", "vc")}
+    dyn = torch.tensor([off_max + 9], dtype=torch.int32, device="cuda")
+    ba.attention_layer(ctx, ws, dev["qp"], dev["kp"], dev["vp"], dev["qn"], dev["kn"], dev["pos"], dev["inv"],
+                       dev["kc"], dev["vc"], off_max, gate=dev["qp"][:, :, D:], dyn=dyn)
+    torch.cuda.synchronize()
+    assert ctx.dyn_overflow() is True
+    assert np.array_equal(cache_np(dev["kc"]), inp["kc"]) and np.array_equal(cache_np(dev["vc"]), inp["vc"])
+
+
 # (T, off, off_max, H, KV, rotate, min prefill blocks): the one-call layer (bn_attn_layer) with a device offset below
 # the host bound on its paths past one row: 8 verify rows (prep_kernel<8, 3> writes q and the K/V rows, then
 # verify_kernel and the merge), 12 rows (prep_kernel, then decodes of their rows with q normed in the prologue), a
