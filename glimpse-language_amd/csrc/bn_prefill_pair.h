@@ -19,7 +19,8 @@
 //   per SIMD keep the matrix cores fed (a wave's LDS reads alone cannot feed one head per wave at full rate).
 //   Pipeline per tile j: S^T(j) on the MFMA units, then O += P(j - 1) V(j - 1) on the MFMA units while the VALU turns
 //   S^T(j) into P(j). K and V have separate 2-stage rings per group in LDS (prefill_kernel's padded row-pair layout);
-//   at the top of tile j the group copies K(j + 1) and V(j) (global_load_lds, no VGPRs), which land during tile j.
+//   K(j + 1) is copied during the S^T phase of tile j and V(j) during its PV phase (global_load_lds, no VGPRs), each
+//   waited for one phase before it is read.
 //   The loop is assembly with a fixed register map (bn_prefill_pair_loop.h): a wave's O, Q^T, S^T and P take about 490
 //   of its 512 registers, more than the compiler's allocator placed without spilling.
 //   Softmax in fp32, log2 domain; the running max moves only when a row's max grows by more than 2^8, so O is rarely
@@ -42,7 +43,7 @@ constexpr int PP_OP = 1040;                      // row pitch (bytes) of the mer
         PP_V10(6), PP_V10(7), PP_V10(8), PP_V10(9), PP_V10(10), PP_V10(11), PP_V10(12), PP_V10(13), PP_V10(14),        \
         PP_V10(15), PP_V10(16), PP_V10(17), PP_V10(18), PP_V10(19), PP_V10(20), PP_V10(21), "v220", "v221", "v222",     \
         "v223", PP_V10(24), "v250", "v251", "v252", "v253", "v254", "v255", "s80", "s81", "s82", "s83", "s84", "s85",   \
-        "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95", "s96", "s97", "vcc", "memory"
+        "s86", "s87", "s88", "s89", "s90", "s91", "s92", "s93", "s94", "s95", "s96", "s97", "s79", "s70", "s71", "s72", "s73", "vcc", "memory"
 
 // O = 0 in the accumulation registers the loop uses (tile (head hh, dims 32 dt ..) in a[16 (8 hh + dt) : +15])
 __device__ __forceinline__ void pp_zero_o(f16x (&o)[2][8]) {
@@ -229,10 +230,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   v_mov_b32 v239, 0
   s_mov_b32 s85, 0
   s_mov_b64 s[92:93], 0
+  s_sub_u32 s70, %[rowb], 1040
+  s_subb_u32 s71, 0, 0
+  s_sub_u32 s72, %[rowb], 1088
+  s_subb_u32 s73, 0, 0
   s_waitcnt lgkmcnt(0)
   s_mov_b32 s84, 0
 .Lppl_loop%=:
+  s_cmp_eq_u32 s84, 0
+  s_cbranch_scc0 .Lppl_topw%=
   s_waitcnt vmcnt(0)
+.Lppl_topw%=:
+  s_waitcnt vmcnt(8)
   s_barrier
   s_cmp_eq_u32 s85, 0
   s_cbranch_scc1 .Lppl_norescale%=
@@ -254,15 +263,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   s_cselect_b32 s83, 1, 0
   s_bitcmp1_b32 s84, 0
   s_cselect_b32 s89, %[vc1], %[vc0]
-  s_mov_b32 s80, s81
-  PPL_CSET %[vlo], %[vhi], s89, 1088, s86, s87, s88
   s_mov_b32 s97, 0
+  s_mov_b32 s79, 0
   s_add_u32 s90, s84, 1
   s_cmp_lt_u32 s90, %[n]
   s_cbranch_scc0 .Lppl_nok%=
   s_bitcmp1_b32 s84, 0
   s_cselect_b32 s96, %[kc0], %[kc1]
   s_add_u32 s80, s81, 1
+  s_mov_b32 s79, 1
   PPL_CSET %[klo], %[khi], s96, 1040, s94, s95, s97
 .Lppl_nok%=:
   s_bitcmp1_b32 s84, 0
@@ -279,15 +288,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   s_branch .Lppl_next%=
 .Lppl_notile%=:
   s_cmp_eq_u32 s84, %[n]
-  s_cbranch_scc0 .Lppl_next%=
+  s_cbranch_scc0 .Lppl_idle%=
   s_cmp_eq_u32 s84, 0
-  s_cbranch_scc1 .Lppl_next%=
+  s_cbranch_scc1 .Lppl_idle%=
   s_bitcmp1_b32 s84, 0
   s_cbranch_scc0 .Lppl_lastodd%=
   PPL_LAST 160, %[vr0]
   s_branch .Lppl_next%=
 .Lppl_lastodd%=:
   PPL_LAST 176, %[vr1]
+  s_branch .Lppl_next%=
+.Lppl_idle%=:
+  s_barrier
 .Lppl_next%=:
   s_add_u32 s84, s84, 1
   s_cmp_le_u32 s84, %[half]
