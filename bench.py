@@ -439,7 +439,7 @@ def cpu_baseline(budget_s=8.0, H=16, KV=4, L=8192, nseq=4):
 ALL = ("decode_8k_batch32", "prefill_4k", "ragged_32", "verify_8", "decode_1k", "prefill_prefix",
        "decode_8k_batch32_rotated", "prefill_4k_rotated", "prefill_4k_f32q", "verify_8_rotated", "prep_4k",
        "prep_decode",
-       "gate_rotate_4k", "verify_8k_4b", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k", "kv_copy_8x4k",
+       "gate_rotate_4k", "verify_8k_4b", "verify_16_8k_4b", "layer_decode_8k", "layer_verify_8", "layer_prefill_4k", "kv_copy_8x4k",
        "qkv_decode_4b", "qkv_verify_8_4b", "qkv_prefill_4k_4b", "o_proj_decode_4b", "o_proj_prefill_4k_4b",
        "block_decode_8k_4b", "block_verify_8_4b", "block_prefill_4k_4b")
 # ternary projections of the 4B layer (hidden 2560, 16 q heads, 4 kv heads): q_proj 8192 rows (q and gate halves),
@@ -501,6 +501,10 @@ def main():
     if "verify_8k_4b" in only:
         log("verify_8k_4b (8 rows over 8184 cached rows, 16/4 heads)")
         res["verify_8k_4b"] = r = W.attn(K, Wm, 16, 4, 8, 8184, ba.KIND_VERIFY, 0xB0A5A10A)
+        log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
+    if "verify_16_8k_4b" in only:
+        log("verify_16_8k_4b (16 rows, the reference's largest verify, over 8176 cached rows, 16/4 heads)")
+        res["verify_16_8k_4b"] = r = W.attn(K, Wm, 16, 4, 16, 8176, ba.KIND_VERIFY, 0xB0A5A10B)
         log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
     if "decode_1k" in only:
         log("decode_1k")

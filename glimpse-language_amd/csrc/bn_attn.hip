@@ -38,7 +38,7 @@ struct bn_ctx {
     int decode_max_splits;
     // blocks flash_kernel's key splits aim at (1 .. kFlashTargetBlocks; BONSAI_ATTN_FLASH_TARGET_BLOCKS)
     int flash_target_blocks;
-    // 2..8 verify rows on verify_kernel (1, the default) or as decodes of their rows (0; BONSAI_ATTN_VERIFY_MFMA)
+    // 2..16 verify rows on verify_kernel (1, the default) or as decodes of their rows (0; BONSAI_ATTN_VERIFY_MFMA)
     int verify_mfma;
     // fp16-q prefills on prefill_kernel (0, the default) or prefill_pair_kernel (1; BONSAI_ATTN_PREFILL_PAIR=1)
     int prefill_pair;
@@ -469,9 +469,9 @@ bn_status run_rows(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, const bn:
 #ifndef BN_VERIFY_BLOCKS
 #define BN_VERIFY_BLOCKS 128
 #endif
-constexpr int kVerifyMfmaMax = 8;  // 4 heads x 8 rows: one 32-column MFMA tile
+constexpr int kVerifyMfmaMax = 16;  // two row groups of 8 (4 heads x 8 rows: one 32-column MFMA tile each)
 
-// verify_kernel's keys per split for 2..8 rows: about BN_VERIFY_BLOCKS blocks over the kv heads, whole 32-key tiles
+// verify_kernel's keys per split for 2..16 rows: about BN_VERIFY_BLOCKS blocks over the kv heads, whole 32-key tiles
 // for each of the W waves, and never more splits than the workspace query sized (its chunk is a lower bound).
 // 0 when the workspace holds no partials (a short context: every row fits one split of the decode path).
 int64_t verify_chunk(const bn_attn_args* a) {
@@ -493,10 +493,12 @@ size_t verify_q_offset(const bn_attn_args* a) {
     return (plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap).total() + 255) / 256 * 256;
 }
 
-// 2..8 rows of one sequence on verify_kernel (every K/V row read once for all rows), then decode_combine_kernel
-// for the merge, the gate and the rotation. The rows' K/V, when given, are appended by verify_kernel itself.
+// 2..16 rows of one sequence on verify_kernel (every K/V row read once per group of 8 rows), then
+// decode_combine_kernel for the merge, the gate and the rotation. The rows' K/V, when given, are appended by
+// verify_kernel itself.
 bn_status run_verify(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int64_t chunk) {
     const int64_t T = a->T, nk = (int64_t)a->off + T, ns = ceil_div(nk, chunk);
+    const unsigned groups = (unsigned)ceil_div(T, 8);
     const int64_t units = 8 * T * ceil_div(ns, 8);
     bn::VerifyArgs v{};
     if (a->flags & BN_Q_F16)
@@ -517,11 +519,11 @@ bn_status run_verify(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a, int64_t
     v.chunk = (int)chunk;
     v.units = (int)units;
     if (v.q)
-        bn_launch(ctx, (bn::verify_kernel<BN_VERIFY_WAVES, true>), dim3((unsigned)ns, (unsigned)a->KV),
-                           dim3(64 * BN_VERIFY_WAVES), 0, st, v);
+        bn_launch(ctx, (bn::verify_kernel<BN_VERIFY_WAVES, true>), dim3((unsigned)ns, (unsigned)a->KV, groups),
+                  dim3(64 * BN_VERIFY_WAVES), 0, st, v);
     else
-        bn_launch(ctx, (bn::verify_kernel<BN_VERIFY_WAVES, false>), dim3((unsigned)ns, (unsigned)a->KV),
-                           dim3(64 * BN_VERIFY_WAVES), 0, st, v);
+        bn_launch(ctx, (bn::verify_kernel<BN_VERIFY_WAVES, false>), dim3((unsigned)ns, (unsigned)a->KV, groups),
+                  dim3(64 * BN_VERIFY_WAVES), 0, st, v);
     bn_status s = launched(ctx, "verify_kernel");
     if (s) return s;
     bn::DecodeArgs d{};
@@ -1250,7 +1252,7 @@ bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, co
     rp.s1 = (int)p->s1;
     rp.s2 = (int)p->s2;
     if (p->T <= (uint32_t)kVerifyMax) {
-        // 2..8 rows: prep_kernel writes q (to p->q in its form, else fp32 into the workspace after the partials)
+        // 2..16 rows: prep_kernel writes q (to p->q in its form, else fp32 into the workspace after the partials)
         // and the K/V rows, then verify_kernel and the merge
         const int64_t chunk = ctx->verify_mfma ? verify_chunk(&m) : 0;
         if (chunk) {

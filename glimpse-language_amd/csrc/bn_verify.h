@@ -1,5 +1,5 @@
-// Speculative verify on fp16 MFMA: 2..8 draft rows of one sequence against the cache, every K/V row read once
-// for all rows.
+// Speculative verify on fp16 MFMA: 2..16 draft rows of one sequence against the cache, every K/V row read once
+// for every 8 rows.
 //
 // Semantics follow attn_split.comp:9-58 + attn_combine.comp:6-21 of the reference: row t (position off+t) of head
 // h attends to cache rows [0, off+t+1) of kv head h/4 (causal among the drafts), softmax(q.k/16) v. The K/V rows
@@ -8,11 +8,13 @@
 // rotation are decode_combine_kernel's.
 //
 // Decomposition (this kernel's own):
-//   The 4 query heads of a kv head times T <= 8 rows are at most 32 query rows: one MFMA column tile. Column
-//   c = 8 hq + t holds row t of head 4 kh + hq (columns t >= T repeat row T-1 and are dropped). Block (split s,
-//   kv head kh) covers keys [s chunk, (s+1) chunk) for all 32 columns; its W waves take contiguous runs of the
-//   split's 32-key tiles, each wave with its own K/V stage in LDS (the tile layout of prefill_kernel: rows p and
-//   p+16 share one 1 KB global_load_lds copy, padded so the operand reads are conflict-free).
+//   The 4 query heads of a kv head times 8 rows are 32 query rows: one MFMA column tile. Block (split s, kv head
+//   kh, row group z) takes rows 8 z .. 8 z + 7 (the reference verifies up to 16 rows: two row groups, each reading
+//   the split's K/V rows once); column c = 8 hq + t' holds row 8 z + t' of head 4 kh + hq (columns past the last
+//   row repeat it and are dropped). The block covers keys [s chunk, (s+1) chunk) for all 32 columns; its W waves
+//   take contiguous runs of the split's 32-key tiles, each wave with its own K/V stage in LDS (the tile layout of
+//   prefill_kernel: rows p and p+16 share one 1 KB global_load_lds copy, padded so the operand reads are
+//   conflict-free).
 //   S^T = K Q^T on v_mfma_f32_32x32x16_f16 (Q^T in registers as fp16; an fp32 q is carried as an fp16 hi/lo
 //   pair, hi = fp16(q), lo = fp16(q - hi), both multiplied into the same accumulator, so its scores keep about
 //   22 of q's 24 bits at any score scale), online softmax in fp32 in the log2 domain (the running max moves only when a column's max grows by more than 2^8), O += P V with P from the
@@ -65,8 +67,9 @@ __global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
     const uint16_t* vb = a.vc + (int64_t)kh * D;
     uint8_t* const st = lds + w * PF_STAGE;
 
-    // this lane's column: row t of head 4 kh + hq; its keys are <= qpos
-    const int hq = r32 >> 3, t = min(r32 & 7, T - 1);
+    // this lane's column: row t of head 4 kh + hq (the block's rows rb .. rb + 7); its keys are <= qpos
+    const int rb = 8 * (int)blockIdx.z;
+    const int hq = r32 >> 3, t = min(rb + (r32 & 7), T - 1);
     const int qpos = off + t;
 
     // Tile copies into this wave's stage, K and V separately: instruction i moves row pair i (rows i, i+16); lane l
@@ -105,29 +108,31 @@ __global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
     float* bc = reinterpret_cast<float*>(bc_lds[w]);
 
     // The call's new rows [off, off + T) that fall in this wave's tiles go to the cache first (fp16, nearest even),
-    // before the wave's copies read them: no other wave or block reads those rows (the tiles partition the keys).
+    // before the wave's copies read them: the tiles partition the keys among the waves and splits, and the blocks of
+    // the other row group write the same bytes to the same rows before reading them.
     if (a.k_new && !dyn_over(a.dyn, a.off)) {  // past the bound nothing is appended (the flag is set)
         const int r0 = max(off, k0 + j_begin * PF_BK), r1 = min(nk, k0 + j_end * PF_BK);
-        if (r0 < r1) {
+        // up to 16 rows, 8 at a time
+        for (int rr = r0; rr < r1; rr += 8) {
             f4 kn[8], vn[8];
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (r0 + i < r1) {
-                    const int64_t src = (int64_t)(r0 + i - off) * kvd + (int64_t)kh * D + 4 * lane;
+                if (rr + i < r1) {
+                    const int64_t src = (int64_t)(rr + i - off) * kvd + (int64_t)kh * D + 4 * lane;
                     kn[i] = *reinterpret_cast<const f4*>(a.k_new + src);
                     vn[i] = *reinterpret_cast<const f4*>(a.v_new + src);
                 }
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (r0 + i < r1) {
-                    const int64_t dst = (int64_t)(r0 + i) * kvd + (int64_t)kh * D + 4 * lane;
+                if (rr + i < r1) {
+                    const int64_t dst = (int64_t)(rr + i) * kvd + (int64_t)kh * D + 4 * lane;
                     const h4 kh4 = {(_Float16)kn[i][0], (_Float16)kn[i][1], (_Float16)kn[i][2], (_Float16)kn[i][3]};
                     const h4 vh4 = {(_Float16)vn[i][0], (_Float16)vn[i][1], (_Float16)vn[i][2], (_Float16)vn[i][3]};
                     *reinterpret_cast<h4*>(a.kc + dst) = kh4;
                     *reinterpret_cast<h4*>(a.vc + dst) = vh4;
                 }
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the rows are in L2 before the copies below read them
         }
+        if (r0 < r1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the rows are in L2 before the copies read them
     }
     // the first tile's copies are in flight while the q rows load
     if (j_begin < j_end) {
@@ -179,7 +184,7 @@ __global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
             issue_k(j + 1);
         }
         // causal mask where a key may pass a column's position; register r holds key j0 + 8(r/4) + 4h + r%4
-        if (j0 + PF_BK - 1 > off) {
+        if (j0 + PF_BK - 1 > off + rb) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int key = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -270,7 +275,7 @@ __global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
         }
     __syncthreads();
     for (int e = tid; e < 32 * 64; e += 64 * W) {
-        const int c = e >> 6, d4 = e & 63, tc = c & 7, hc = c >> 3;
+        const int c = e >> 6, d4 = e & 63, tc = rb + (c & 7), hc = c >> 3;
         if (tc >= T || k0 > off + tc) continue;
         float M = ml_lds[0][0][c];
 #pragma unroll

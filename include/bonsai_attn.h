@@ -80,7 +80,7 @@ typedef struct bn_attn_args {
     float* out;         /* [T][H][256] fp32 gated attention output (rotated when `signs` is set) */
     int64_t o_ts, o_hs;
 
-    void* ws;        /* device workspace (split partials; for bn_attn_layer with 2..8 rows also their fp16 q),
+    void* ws;        /* device workspace (split partials; for bn_attn_layer with 2..16 rows also their q),
                         >= bn_attn_workspace_size(args) bytes, 16-byte
                         aligned; NULL when the size is 0. No initialisation is needed and nothing in it
                         outlives the call. Calls that overlap in time on one workspace race. */
@@ -341,14 +341,15 @@ bn_status bn_gate_rotate(bn_ctx* ctx, bn_stream stream, const bn_rotate_args* a)
 /* The attention arm of one layer in one call (model.rs:828-893: attn_prep, attn_split, attn_combine, gate_rotate):
  * p's raw rows (q_proj's q half, k_proj, v_proj) are normed and rotated as bn_attn_prep does, the K/V rows land
  * in the cache, and `a` attends, gates and (with a->signs) rotates. One row (a decode step) runs attn_prep inside
- * the decode kernel's prologue: one split launch, plus the split merge when the keys are split. 2..8 rows whose
+ * the decode kernel's prologue: one split launch, plus the split merge when the keys are split. 2..16 rows whose
  * keys the workspace splits (verify drafts) have q and the K/V rows written by the prep kernel (q to p->q in p's
- * form when given, else fp32 into the workspace), then the verify kernel and the merge. Other rows up to 16 run as decodes
- * of their rows with q normed in the prologue, their K/V rows written by the prep kernel first. For T > 16 (prefill) the
+ * form when given, else fp32 into the workspace), then the verify kernel and the merge. Other rows up to 16 (short
+ * contexts) run as decodes of their rows with q normed in the prologue, their K/V rows written by the prep kernel
+ * first. For T > 16 (prefill) the
  * prep kernel writes q to p->q (fp16 with BN_Q_F16, the faster form for the prefill kernels) and the K/V rows,
  * then the prefill kernels run. p and a describe the same rows (T, off, H, KV, cap, kc, vc); a->q, a->k_new and
  * a->v_new are NULL and a->flags is 0. p->q is needed only for T > 16; otherwise it may be NULL (when given for
- * 2..8 rows it receives q). Same workspace as bn_attn_forward. */
+ * 2..16 rows it receives q). Same workspace as bn_attn_forward. */
 bn_status bn_attn_layer(bn_ctx* ctx, bn_stream stream, const bn_prep_args* p, const bn_attn_args* a);
 
 /* ---- ternary projections either side of the attention call ------------------------------------------ */

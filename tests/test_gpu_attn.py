@@ -116,15 +116,16 @@ def test_verify_8_workload(gpu):
     check_case(gpu, inp, ba.KIND_VERIFY)
 
 
-# (2, 0), (3, 17): short contexts, rows as decodes of one split; (16, 1000): more rows than one MFMA tile holds;
-# the rest run on verify_kernel: one split (2, 63), a partial last tile (6, 129), many splits
-@pytest.mark.parametrize("T,off", [(2, 0), (3, 17), (16, 1000), (5, 4095), (2, 63), (6, 129), (7, 1000), (8, 9000)])
+# (2, 0), (3, 17): short contexts, rows as decodes of one split; the rest run on verify_kernel: one split (2, 63), a
+# partial last tile (6, 129), many splits; 9..16 rows as two row groups (the second one partial for 9 and 12 rows)
+@pytest.mark.parametrize("T,off", [(2, 0), (3, 17), (16, 1000), (5, 4095), (2, 63), (6, 129), (7, 1000), (8, 9000),
+                                   (9, 500), (12, 3000), (16, 70), (15, 9000)])
 def test_verify_shapes(gpu, T, off):
     inp = workload.layer(900 + T + off, T=T, off=off, H=8, KV=2)
     check_case(gpu, inp, ba.KIND_VERIFY)
 
 
-@pytest.mark.parametrize("T,off,gate", [(8, 8191, True), (3, 2000, False), (4, 250, True)])
+@pytest.mark.parametrize("T,off,gate", [(8, 8191, True), (3, 2000, False), (4, 250, True), (16, 8176, True)])
 def test_verify_4b_heads(gpu, T, off, gate):
     inp = workload.layer(950 + T + off, T=T, off=off, H=16, KV=4, gate=gate)
     check_case(gpu, inp, ba.KIND_VERIFY)
@@ -146,13 +147,14 @@ def test_verify_rows_equal_decodes(gpu):
         assert np.max(np.abs(o.cpu().numpy()[0] - out[t])) <= 2e-4
 
 
-def test_verify_kernel_equals_rows_path(gpu):
-    """verify_kernel (all rows of a kv head in one MFMA tile, each K/V row read once) against the same call run as
-    decodes of its rows (BONSAI_ATTN_VERIFY_MFMA=0): both carry the reference's semantics, and differ only by the
-    fp16 rounding of q in the MFMA scores (a few 1e-5); 2e-4 bounds it."""
+@pytest.mark.parametrize("T", [8, 16])
+def test_verify_kernel_equals_rows_path(gpu, T):
+    """verify_kernel (8 rows of a kv head in one MFMA tile, each K/V row read once per 8 rows) against the same call
+    run as decodes of its rows (BONSAI_ATTN_VERIFY_MFMA=0): both carry the reference's semantics, and differ only by
+    the fp16 rounding of q in the MFMA scores (a few 1e-5); 2e-4 bounds it."""
     from conftest import context_with
     torch, ctx, ws = gpu
-    inp = workload.layer(0x9500, T=8, off=8184, H=16, KV=4)
+    inp = workload.layer(0x9500 + T, T=T, off=8192 - T, H=16, KV=4)
     out, d = run(gpu, inp, ba.KIND_VERIFY)
     ctx0 = context_with(BONSAI_ATTN_VERIFY_MFMA=0)
     ws0 = ba.Workspace(ctx0, "cuda")
