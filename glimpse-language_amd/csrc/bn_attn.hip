@@ -42,6 +42,9 @@ struct bn_ctx {
     int verify_mfma;
     // fp16-q prefills on prefill_kernel (0, the default) or prefill_pair_kernel (1; BONSAI_ATTN_PREFILL_PAIR=1)
     int prefill_pair;
+    // 17..64 rows too few for prefill_kernel: verify_kernel's row groups (1, the default) or flash_kernel (0;
+    // BONSAI_ATTN_MID_ROWS)
+    int mid_rows;
     // this device's copy of `scratch` (the partials of bn_attn_decode_ragged_noalloc), or null if its address
     // could not be taken
     void* scratch;
@@ -649,7 +652,43 @@ bn_status rotate_in_place(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
     return launched(ctx, "rotate_kernel");
 }
 
+// 17..64 rows that do not fill the GPU with prefill_kernel's q-tiles: verify_kernel over row groups of 8 rows (32
+// query rows of a kv head per block, q read once per key split) after append_kernel writes the rows. flash_kernel
+// has only one or two 32-token q-tiles per kv head there, so its parallelism comes from key splits that each reload
+// the q-tile and write 128 rows of partials: measured 16.5 against 30 us for 33 rows over 5 cached keys (8/2 heads)
+// and 36 against 71 us for 64 rows over 8,000 keys (16/4); from 100 rows up flash_kernel is faster (25 against
+// 30 us at 100 rows over 300 keys, 28 against 33 us at 256 over 512), since each of its blocks stages a K/V tile
+// once for 128 query rows where a row group uses it for 32. Keys per split: about kMidTargetBlocks blocks over the
+// kv heads and row groups, whole 32-key tiles for each of the W waves.
+constexpr int64_t kMidTargetBlocks = 256;
+constexpr uint32_t kMidMaxRows = 64;
+bool use_mid_rows(const bn_ctx* ctx, const bn_attn_args* a) {
+    return ctx->mid_rows && a->T > (uint32_t)kVerifyMax && a->T <= kMidMaxRows &&
+           !use_prefill(a, ctx->prefill_min_blocks);
+}
+int64_t mid_chunk(const bn_attn_args* a) {
+    const int64_t T = a->T, nk = (int64_t)a->off + T, groups = ceil_div(T, 8);
+    int64_t ns = ceil_div(kMidTargetBlocks, (int64_t)a->KV * groups);
+    if (ns < 1) ns = 1;
+    const int64_t step = 32 * BN_VERIFY_WAVES;
+    return ceil_div(ceil_div(nk, ns), step) * step;
+}
+size_t mid_records_bytes(const bn_attn_args* a) {
+    const int64_t T = a->T, ns = ceil_div((int64_t)a->off + T, mid_chunk(a));
+    return (size_t)(a->KV * 8 * T * ceil_div(ns, 8)) * bn::DEC_PART * sizeof(float);
+}
+
 bn_status run_flash(bn_ctx* ctx, hipStream_t st, const bn_attn_args* a) {
+    if (use_mid_rows(ctx, a)) {
+        bn_attn_args m = *a;
+        if (a->k_new) {
+            bn_status s = launch_append(ctx, st, a);
+            if (s) return s;
+            m.k_new = nullptr;
+            m.v_new = nullptr;
+        }
+        return run_verify(ctx, st, &m, mid_chunk(a));
+    }
     const bool fused = use_prefill(a, ctx->prefill_min_blocks);  // prefill_kernel rotates in its epilogue
     bn_status s = attend_flash(ctx, st, a);
     if (s || !a->signs || fused) return s;
@@ -1047,6 +1086,8 @@ bn_status bn_ctx_create(int device, bn_ctx** out) {
     if (const char* e = getenv("BONSAI_ATTN_VERIFY_MFMA")) c->verify_mfma = atoi(e) != 0;
     c->prefill_pair = 0;
     if (const char* e = getenv("BONSAI_ATTN_PREFILL_PAIR")) c->prefill_pair = atoi(e) != 0;
+    c->mid_rows = 1;
+    if (const char* e = getenv("BONSAI_ATTN_MID_ROWS")) c->mid_rows = atoi(e) != 0;
     c->scratch = scratch_address(device);
     c->launch_err = hipSuccess;
     c->err[0] = 0;
@@ -1063,8 +1104,13 @@ size_t bn_attn_workspace_size(const bn_attn_args* a) {
     size_t rows = a->T <= (uint32_t)kVerifyMax ? plan_rows(a, 1, BN_DECODE_MAX_TARGET_WAVES, kMaxSplitsCap).total() : 0;
     if (verify_chunk(a)) rows = verify_q_offset(a) + (size_t)a->T * a->H * bn::D * sizeof(float);
     if (a->T == 1) return rows;
-    // the kernel choice for T >= 2 depends on the context, so the size covers the flash kernel's partials
-    const size_t fl = plan_flash(a->T, a->off, a->KV).total();
+    // the kernel choice for T >= 2 depends on the context, so the size covers the flash kernel's partials and, for
+    // more than 16 rows, verify_kernel's row-group records
+    size_t fl = plan_flash(a->T, a->off, a->KV).total();
+    if (a->T > (uint32_t)kVerifyMax && a->T <= kMidMaxRows) {
+        const size_t mid = mid_records_bytes(a);
+        if (mid > fl) fl = mid;
+    }
     return fl > rows ? fl : rows;
 }
 

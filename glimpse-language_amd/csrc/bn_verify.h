@@ -69,6 +69,9 @@ __global__ __launch_bounds__(64 * W) void verify_kernel(VerifyArgs a) {
 
     // this lane's column: row t of head 4 kh + hq (the block's rows rb .. rb + 7); its keys are <= qpos
     const int rb = 8 * (int)blockIdx.z;
+    // a split that starts past the row group's last position holds no key of its rows (nor a new row: the last row
+    // group, which covers every split that holds one, appends those)
+    if (k0 > off + min(rb + 7, T - 1)) return;
     const int hq = r32 >> 3, t = min(rb + (r32 & 7), T - 1);
     const int qpos = off + t;
 

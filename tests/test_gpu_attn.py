@@ -163,6 +163,27 @@ def test_verify_kernel_equals_rows_path(gpu, T):
     assert np.max(np.abs(rows.cpu().numpy() - out)) <= 2e-4
 
 
+@pytest.mark.parametrize("T,off,H,KV", [(40, 3000, 16, 4), (64, 100, 8, 2), (17, 0, 4, 1)])
+def test_mid_rows_equal_flash(gpu, T, off, H, KV):
+    """17..64 rows take verify_kernel's row groups of 8 (BONSAI_ATTN_MID_ROWS, on by default) instead of
+    flash_kernel: both against the oracle, and against each other within 2e-4 (both carry an fp32 q as an fp16 hi/lo
+    pair; they differ in the order of the sums)."""
+    from conftest import context_with
+    torch, ctx, ws = gpu
+    inp = workload.layer(0x9700 + T + off, T=T, off=off, H=H, KV=KV)
+    print(f"mid rows vs flash: T={T} off={off} H={H} KV={KV}", flush=True)
+    err = check_case(gpu, inp, ba.KIND_PREFILL)
+    out, d = run(gpu, inp, ba.KIND_PREFILL, append=False)
+    ctx0 = context_with(BONSAI_ATTN_MID_ROWS=0)
+    ws0 = ba.Workspace(ctx0, "cuda")
+    fl = ba.attention(ctx0, ws0, d["q"], d["kc"], d["vc"], inp["off"], gate=d["gate"], kind=ba.KIND_PREFILL)
+    torch.cuda.synchronize()
+    diff = float(np.max(np.abs(fl.cpu().numpy() - out)))
+    print(f"mid rows vs flash: oracle max-abs {err:.3e}, paths differ by {diff:.3e}", flush=True)
+    assert diff <= 2e-4
+    ctx0.close()
+
+
 def test_prefill_prefix_workload(gpu):
     inp = workload.layer(workload.SEED_BASE + 1, **workload.WORKLOADS["prefill_prefix"])
     err = check_case(gpu, inp, ba.KIND_PREFILL)
