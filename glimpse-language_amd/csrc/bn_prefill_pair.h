@@ -88,8 +88,8 @@ __device__ __forceinline__ void pp_dump_o(f16x (&o)[2][8], uint32_t obase) {
 }
 // The merge of head HH in place: staging = O fo + staging fx per row (O: this wave's, staging: the partner's dump),
 // the 16 factors of a lane's register rows read from bc (fo at bc + 32 q + 16 (l / 32) into v32-v47, fx 128 bytes on
-// into v48-v63). The partner's values of two dim tiles are in flight at a time (v0-v31): tile dt + 2 is requested
-// into tile dt's registers as soon as they are used.
+// into v48-v63). The partner's values of dim tile dt + 1 are requested (into the other half of v0-v31) as soon as
+// tile dt's have landed, so their latency passes under tile dt's arithmetic; every wait drains the LDS counter.
 template <int HH>
 __device__ __forceinline__ void pp_merge_o(f16x (&o)[2][8], uint32_t obase, uint32_t bc) {
     asm volatile(R"ASM(
@@ -101,15 +101,15 @@ __device__ __forceinline__ void pp_merge_o(f16x (&o)[2][8], uint32_t obase, uint
     ds_read_b128 v[32+4*\q:35+4*\q], %[bc] offset:32*\q
     ds_read_b128 v[48+4*\q:51+4*\q], %[bc] offset:128+32*\q
   .endr
-  .irp dt, 0,1
-    .irp r, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15
-      ds_read_b32 v[16*\dt+\r], %[ob] offset:(32*%[hh]+8*((\r)>>2)+((\r)&3))*1040+128*\dt
-    .endr
+  .irp r, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15
+    ds_read_b32 v[\r], %[ob] offset:(32*%[hh]+8*((\r)>>2)+((\r)&3))*1040
   .endr
-  s_waitcnt lgkmcnt(0)
   .irp dt, 0,1,2,3,4,5,6,7
-    .if \dt >= 2
-      s_waitcnt lgkmcnt(15)
+    s_waitcnt lgkmcnt(0)
+    .if \dt < 7
+      .irp r, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15
+        ds_read_b32 v[16*(((\dt)+1)&1)+\r], %[ob] offset:(32*%[hh]+8*((\r)>>2)+((\r)&3))*1040+128*(\dt+1)
+      .endr
     .endif
     .irp r, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15
       v_accvgpr_read_b32 v[64+((\r)&7)], a[16*(8*%[hh]+\dt)+\r]
@@ -117,11 +117,6 @@ __device__ __forceinline__ void pp_merge_o(f16x (&o)[2][8], uint32_t obase, uint
       v_fmac_f32 v[64+((\r)&7)], v[16*((\dt)&1)+\r], v[48+\r]
       ds_write_b32 %[ob], v[64+((\r)&7)] offset:(32*%[hh]+8*((\r)>>2)+((\r)&3))*1040+128*\dt
     .endr
-    .if \dt < 6
-      .irp r, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15
-        ds_read_b32 v[16*((\dt)&1)+\r], %[ob] offset:(32*%[hh]+8*((\r)>>2)+((\r)&3))*1040+128*(\dt+2)
-      .endr
-    .endif
   .endr
   s_waitcnt lgkmcnt(0)
 )ASM" ::[ob] "v"(obase), [bc] "v"(bc), [hh] "n"(HH), PP_O_INPUTS(o)
