@@ -276,12 +276,12 @@ __device__ __forceinline__ int tern_swz(int m, int k) {
 
 // Block -> (row tile rt, token tile tt). Workgroups are dealt to the 8 XCDs round robin (block b on XCD b % 8), and
 // each XCD has its own L2. When the token tiles divide evenly, XCD x takes the token tiles x, x + 8, ... in groups of
-// BN_TERN_XCD_GROUP and runs every row tile of a group before the next group, the group's token tiles of one row tile
-// on consecutive blocks: each x tile is fetched into one L2 (and stays there while the row tiles pass), and each row
+// G (BN_TERN_XCD_GROUP by default; tern_pf_kernel's 128-token blocks take half as many, so a group spans the same
+// tokens) and runs every row tile of a group before the next group, the group's token tiles of one row tile on
+// consecutive blocks: each x tile is fetched into one L2 (and stays there while the row tiles pass), and each row
 // tile's codes serve the group from that L2. Otherwise row tiles run fastest (token tile by token tile).
-template <int BM>
+template <int BM, int G = BN_TERN_XCD_GROUP>
 __device__ __forceinline__ void tern_tile(int b, int row_tiles, int T, int& rt, int& tt) {
-    constexpr int G = BN_TERN_XCD_GROUP;
     const int ntt = (T + BM - 1) / BM;
     if (G < 1 || (ntt & 7) || ntt < 16) {
         rt = b % row_tiles;

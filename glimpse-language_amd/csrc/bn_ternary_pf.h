@@ -8,13 +8,14 @@
 // remainder there and the tile's flag word is set: the GEMM then runs that chunk's scaled pass from x itself, as
 // tern_mfma_kernel does.
 //
-// tern_pf_kernel<S, OCC>: S copy stages, OCC blocks per CU (3 stages take 63 KB of LDS: two blocks per CU; 2 stages
-// 42 KB: three). Block = 4 waves x 64 rows (256 rows) x one 64-token tile; for each 64-column chunk every
-// wave copies a quarter of the x tile, its 64 rows' code words and their scale words into one of S LDS stages with
-// global_load_lds, S - 1 chunks ahead of the chunk's 32 MFMAs (2 token tiles x 2 row tiles x 4 k-steps x hi/lo).
-// The copies hold no VGPRs and the block splits nothing: what is left on the VALU is the weight decode. One barrier
-// per chunk: past it, the copies of every wave for the chunk have landed (each wave waited for its own first) and
-// every wave is done with the previous chunk's stage, which the copies issued next then fill.
+// tern_pf_kernel<S, OCC, MT>: S copy stages, OCC blocks per CU, MT 32-token tiles per wave. Block = 4 waves x 64
+// rows (256 rows) x 32 MT tokens (MT / 2 x tiles); for each 64-column chunk every wave copies a quarter of each x tile,
+// its 64 rows' code words and their scale words into one of S LDS stages with global_load_lds, S - 1 chunks ahead of
+// the chunk's 16 MT MFMAs (MT token tiles x 2 row tiles x 4 k-steps x hi/lo). The copies hold no VGPRs and the block
+// splits nothing: what is left on the VALU is the weight decode, once per code word and block, so MT = 4 halves it
+// per MFMA (2 stages of 37 KB: two blocks per CU; MT = 2 with 2 stages of 21 KB: three). One barrier per chunk: past
+// it, the copies of every wave for the chunk have landed (each wave waited for its own first) and every wave is done
+// with the previous chunk's stage, which the copies issued next then fill.
 //
 // The sums are those of tern_mfma_kernel for the same shapes (same split, same k order, same MFMA order): the two
 // give identical results.
@@ -27,9 +28,6 @@ constexpr int TPF_BM = 64;                                    // tokens per tile
 constexpr int TPF_KC = 64;                                    // columns per chunk
 constexpr int TPF_NQ = TPF_KC / 16;                           // MFMA k-steps per chunk
 constexpr int TPF_TILE = 2 * TPF_NQ * 2 * TPF_BM * 16;        // bytes of one (token tile, chunk): hi, then lo
-constexpr int TPF_ST_W = TPF_TILE;                            // stage: the x tile, code words, scale words
-constexpr int TPF_ST_S = TPF_ST_W + 4 * 1024;
-constexpr int TPF_STAGE = TPF_ST_S + 4 * 256;
 
 // (token tile, chunk) tiles of a call; the workspace holds them, then one flag word per tile
 __host__ __device__ inline size_t tern_pf_tiles(int T, int K) {
@@ -88,10 +86,12 @@ __device__ __forceinline__ void tpf_copy4(const void* g, const uint8_t* lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(la) : "memory");
 }
 
-// copies per wave and chunk: 4 of the x tile, 1 of code words, 1 of scale words
-constexpr int TPF_COPIES = 6;
+// copies per wave and chunk: 4 per 64-token x tile, 1 of code words, 1 of scale words
+__host__ __device__ constexpr int tpf_copies(int MT) { return 4 * (MT / 2) + 2; }
+// stage bytes: the block's x tiles (MT / 2 of them), the code words (4 waves x 64 rows x 16 B), the scale words
+__host__ __device__ constexpr int tpf_stage(int MT) { return (MT / 2) * TPF_TILE + 4 * 1024 + 4 * 256; }
 
-template <int S>
+template <int S, int C>
 __device__ __forceinline__ void tpf_wait_barrier() {
     static_assert(S == 2 || S == 3, "stages");
     // this wave's copies of the current chunk have landed (the S - 2 later chunks' copies may be in flight), then
@@ -99,18 +99,22 @@ __device__ __forceinline__ void tpf_wait_barrier() {
     if constexpr (S == 2)
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     else
-        asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
-    static_assert(TPF_COPIES == 6, "the wait count above");
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(C) : "memory");
 }
 
-template <int S, int OCC>
+// MT 32-token tiles per wave: MT = 2 covers one 64-token x tile per block, MT = 4 two (each code word decoded once
+// feeds twice the MFMAs)
+template <int S, int OCC, int MT = 2>
 __global__ __launch_bounds__(256, OCC) void tern_pf_kernel(TernArgs a, int row_tiles, const uint8_t* __restrict__ work) {
-    constexpr int BM = TPF_BM, NQ = TPF_NQ, KC = TPF_KC, MT = 2;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[S * TPF_STAGE];
+    static_assert(MT == 2 || MT == 4, "token tiles per wave");
+    constexpr int BM = 32 * MT, NQ = TPF_NQ, KC = TPF_KC, NX = MT / 2;
+    constexpr int STAGE = tpf_stage(MT), ST_W = NX * TPF_TILE, ST_S = ST_W + 4 * 1024;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S * STAGE];
     const int lane = (int)threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     int rt, tt;
-    tern_tile<BM>((int)blockIdx.x, row_tiles, a.T, rt, tt);
+    tern_tile<BM, (BN_TERN_XCD_GROUP * 64 / BM > 0 ? BN_TERN_XCD_GROUP * 64 / BM : 1)>((int)blockIdx.x, row_tiles,
+                                                                                       a.T, rt, tt);
     const int t0 = tt * BM;
     const int rbase_g = (rt * 4 + wave) * 64;  // first global row of this wave
     const bool active = rbase_g < a.rows;
@@ -118,26 +122,44 @@ __global__ __launch_bounds__(256, OCC) void tern_pf_kernel(TernArgs a, int row_t
     const int mi = tern_member(a, rbase);
     const TernMat m = tern_mat(a, mi);
     const int K = a.K, kw = K >> 4, kg = K >> 7, nchunk = K / KC;
-    const uint8_t* tiles = work + (size_t)tt * nchunk * TPF_TILE;
-    const uint32_t* flags = reinterpret_cast<const uint32_t*>(work + tern_pf_tiles(a.T, K) * TPF_TILE) + (size_t)tt * nchunk;
+    const int nxt = (a.T + TPF_BM - 1) / TPF_BM;  // 64-token x tiles of the call
+    // x tile u of the block: 64-token tile NX tt + u (a tile past the last repeats the last: its tokens are not
+    // stored)
+    const uint8_t* tiles[NX];
+    const uint32_t* flags[NX];
+#pragma unroll
+    for (int u = 0; u < NX; ++u) {
+        const int xt = min(NX * tt + u, nxt - 1);
+        tiles[u] = work + (size_t)xt * nchunk * TPF_TILE;
+        flags[u] = reinterpret_cast<const uint32_t*>(work + tern_pf_tiles(a.T, K) * TPF_TILE) + (size_t)xt * nchunk;
+    }
 
     // the copies of chunk j into stage st
-    const uint8_t* xsrc = tiles + wave * 4096 + lane * 16;
     const uint8_t* wsrc = reinterpret_cast<const uint8_t*>(m.w + (int64_t)(rbase + lane) * kw);  // row rbase + lane
     const uint16_t* ssrc = m.s + (int64_t)(rbase + lane) * kg;
     auto issue = [&](int j, int st) __attribute__((always_inline)) {
-        const uint8_t* sb = lds + st * TPF_STAGE;
+        const uint8_t* sb = lds + st * STAGE;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) tpf_copy16(xsrc + (size_t)j * TPF_TILE + i * 1024, sb + wave * 4096 + i * 1024);
-        tpf_copy16(wsrc + j * 16, sb + TPF_ST_W + wave * 1024);  // the row's 4 code words of the chunk
+        for (int u = 0; u < NX; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                tpf_copy16(tiles[u] + (size_t)j * TPF_TILE + wave * 4096 + i * 1024 + lane * 16,
+                           sb + u * TPF_TILE + wave * 4096 + i * 1024);
+        tpf_copy16(wsrc + j * 16, sb + ST_W + wave * 1024);  // the row's 4 code words of the chunk
         // the 4-byte word holding the row's scale of the chunk (the scale array is 4-byte aligned with an even count)
         const uintptr_t sp = reinterpret_cast<uintptr_t>(ssrc + ((j * KC) >> 7));
-        tpf_copy4(reinterpret_cast<const void*>(sp & ~(uintptr_t)3), sb + TPF_ST_S + wave * 256);
+        tpf_copy4(reinterpret_cast<const void*>(sp & ~(uintptr_t)3), sb + ST_S + wave * 256);
+    };
+    auto chunk_big = [&](int j) __attribute__((always_inline)) {
+        uint32_t f = 0;
+#pragma unroll
+        for (int u = 0; u < NX; ++u) f |= flags[u][j];
+        return f != 0;
     };
 
     // whether some chunk of this token tile holds a value >= TERN_BIG (its scaled pass), read before the copies
     int big_local = 0;
-    for (int j = lane; j < nchunk; j += 64) big_local |= flags[j] != 0;
+    for (int j = lane; j < nchunk; j += 64) big_local |= chunk_big(j);
     const bool tile_big = __ballot(big_local) != 0;
 #pragma unroll
     for (int j = 0; j < S - 1; ++j) issue(min(j, nchunk - 1), j);
@@ -163,7 +185,8 @@ __global__ __launch_bounds__(256, OCC) void tern_pf_kernel(TernArgs a, int row_t
             h8 ah[MT], al[MT];
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                const int off = ((q * 2 + kgl) * BM + tern_swz<NQ>(32 * i + n, q * 2 + kgl)) * 8;
+                const int off = (i >> 1) * (TPF_TILE / 2) +
+                                ((q * 2 + kgl) * TPF_BM + tern_swz<NQ>(32 * (i & 1) + n, q * 2 + kgl)) * 8;
                 ah[i] = *reinterpret_cast<const h8*>(xl + off);
                 al[i] = *reinterpret_cast<const h8*>(xl + TPF_TILE / 4 + off);
             }
@@ -179,29 +202,29 @@ __global__ __launch_bounds__(256, OCC) void tern_pf_kernel(TernArgs a, int row_t
     };
 
     for (int c = 0; c < nchunk; ++c) {
-        tpf_wait_barrier<S>();
+        tpf_wait_barrier<S, tpf_copies(MT)>();
         issue(min(c + S - 1, nchunk - 1), (c + S - 1) % S);  // into the stage the previous chunk used
-        uint8_t* sb = lds + (c % S) * TPF_STAGE;
+        uint8_t* sb = lds + (c % S) * STAGE;
         // code words of rows n and 32 + n, and their scales
         u4 wc[2];
         TernTab tab[2];
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
             const int r = 32 * nt + n;
-            wc[nt] = *reinterpret_cast<const u4*>(sb + TPF_ST_W + wave * 1024 + r * 16);
+            wc[nt] = *reinterpret_cast<const u4*>(sb + ST_W + wave * 1024 + r * 16);
             const int half = (int)(((int64_t)(rbase + r) * kg + ((c * KC) >> 7)) & 1);
-            tab[nt] = tern_table(*reinterpret_cast<const uint16_t*>(sb + TPF_ST_S + wave * 256 + r * 4 + half * 2));
+            tab[nt] = tern_table(*reinterpret_cast<const uint16_t*>(sb + ST_S + wave * 256 + r * 4 + half * 2));
         }
         if (active) mfma_chunk(sb, wc, tab);
-        if (tile_big && flags[c]) {
+        if (tile_big && chunk_big(c)) {
             // rare: some token of the tile has a value beyond fp16's range in this chunk (uniform over the block).
             // Its x, times 2^-16, is multiplied into acc times 2^-16, and acc is scaled back: acc + 2^16 (x 2^-16) W^T,
-            // every scaling a power of two (exact). The stage's x tile is free once every wave is past its MFMAs;
+            // every scaling a power of two (exact). The stage's x tiles are free once every wave is past its MFMAs;
             // the copies that refill the stage wait for the next chunk's barrier.
             __syncthreads();
             _Float16* xl = reinterpret_cast<_Float16*>(sb);
 #pragma unroll 1
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < MT; ++i) {
                 const int u = (int)threadIdx.x + 256 * i, mm = u >> 3, q = (u >> 1) & 3, kgu = u & 1;
                 const bool valid = t0 + mm < a.T;
                 const float* p = a.x + (int64_t)min(t0 + mm, a.T - 1) * a.x_ts + c * KC + 16 * q + 4 * kgu;
@@ -209,7 +232,8 @@ __global__ __launch_bounds__(256, OCC) void tern_pf_kernel(TernArgs a, int row_t
                 const bool big = tern_token_big<NQ>(va, vb, valid);
                 h8 hi, lo;
                 tern_split8(va, vb, big ? 2 : 3, hi, lo);
-                const int off = ((q * 2 + kgu) * BM + tern_swz<NQ>(mm, q * 2 + kgu)) * 8;
+                const int off = (mm >> 6) * (TPF_TILE / 2) +
+                                ((q * 2 + kgu) * TPF_BM + tern_swz<NQ>(mm & 63, q * 2 + kgu)) * 8;
                 *reinterpret_cast<h8*>(xl + off) = hi;
                 *reinterpret_cast<h8*>(xl + TPF_TILE / 4 + off) = lo;
             }

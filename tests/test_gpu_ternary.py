@@ -118,9 +118,11 @@ def test_ternary_split_once_matches_in_place(gpu, T, K, os):
 
 
 def test_ternary_split_once_large_grid(gpu):
-    """A split-once call whose grid exceeds three blocks per CU (1,300 tokens x 10,240 rows: 840 blocks) takes the
-    3-stage form of tern_pf_kernel, the smaller shapes above the 2-stage form: bit-identical to the in-place kernel,
-    and the first 64 rows of each matrix checked against the oracle."""
+    """A split-once call whose grid of 64-token blocks exceeds three per CU (1,300 tokens x 10,240 rows: 840 blocks)
+    takes the 128-token blocks of tern_pf_kernel (two x tiles per block; 21 x tiles, so the last block has one and a
+    short one), the smaller shapes above the 64-token blocks: bit-identical to the in-place kernel, and the first 64
+    rows of each matrix checked against the oracle. Then the same with a few x values beyond fp16's range, in a token
+    of each x tile of one block and in the last token (the scaled pass over both of a block's x tiles)."""
     torch, ctx, _ = gpu
     T, K, os = 1300, 2560, (8192, 1024, 1024)
     print(f"ternary split-once large grid T={T}", flush=True)
@@ -130,6 +132,12 @@ def test_ternary_split_once_large_grid(gpu):
     assert all(np.array_equal(a, b) for a, b in zip(got, ref)), "split-once and in-place results differ"
     head = [(w[:64], sc[:64], codes[:64]) for w, sc, codes in mats]
     check([g[:, :64] for g in got], expected(head, x, K), head, x, K, "large grid, first rows")
+    print(f"ternary split-once large grid T={T}, x beyond fp16", flush=True)
+    x = x.copy()
+    x[130, 7], x[200, 1500], x[T - 1, K - 1] = 1.0e5, -7.0e6, 4.0e4
+    got = run_gpu(torch, ctx, mats, x, K, work=True)
+    ref = run_gpu(torch, ctx, mats, x, K)
+    assert all(np.array_equal(a, b) for a, b in zip(got, ref)), "split-once and in-place results differ (large x)"
 
 
 def test_ternary_workspace_with_unaligned_scales(gpu):
