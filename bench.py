@@ -484,9 +484,9 @@ def main():
         log(f"  {r['gbs']:.1f} GB/s ({r['ms'] * 1e3:.1f} us/step)")
     if "prefill_4k" in only:
         log("prefill_4k")
-        res["prefill_4k"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
+        res["prefill_4k"] = r = W.attn(K, Wm, 16, 4, 4096, 0, ba.KIND_PREFILL,
                                        0xB0A5A103, q_f16=True)
-        r["steps"], r["warmup"] = max(2, K // 4), max(1, Wm // 2)
+        r["steps"], r["warmup"] = K, Wm
         log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
     if "ragged_32" in only:
         lens = ragged_lengths()
@@ -520,12 +520,12 @@ def main():
         log(f"  {r['gbs']:.1f} GB/s ({r['ms'] * 1e3:.1f} us/step)")
     if "prefill_4k_rotated" in only:
         log("prefill_4k_rotated")
-        res["prefill_4k_rotated"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
+        res["prefill_4k_rotated"] = r = W.attn(K, Wm, 16, 4, 4096, 0, ba.KIND_PREFILL,
                                                0xB0A5A103, q_f16=True, rotate=True)
         log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
     if "prefill_4k_f32q" in only:
         log("prefill_4k_f32q (fp32 q: the reference's precision, fp16 hi/lo pair on prefill_hilo_kernel)")
-        res["prefill_4k_f32q"] = r = W.attn(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0, ba.KIND_PREFILL,
+        res["prefill_4k_f32q"] = r = W.attn(K, Wm, 16, 4, 4096, 0, ba.KIND_PREFILL,
                                             0xB0A5A103, q_f16=False)
         log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
     if "verify_8_rotated" in only:
@@ -554,7 +554,7 @@ def main():
         log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s")
     if "layer_prefill_4k" in only:
         log("layer_prefill_4k")
-        res["layer_prefill_4k"] = r = W.layer(max(2, K // 4), max(1, Wm // 2), 16, 4, 4096, 0)
+        res["layer_prefill_4k"] = r = W.layer(K, Wm, 16, 4, 4096, 0)
         log(f"  {r['tflops']:.1f} TFLOP/s ({r['ms']:.3f} ms/step)")
     if "kv_copy_8x4k" in only:
         log("kv_copy_8x4k")
@@ -563,15 +563,13 @@ def main():
     for name, cfg in TERNARY.items():
         if name in only:
             log(name)
-            big = cfg["T"] > 16
-            res[name] = r = W.ternary(max(2, K // 4) if big else K, max(1, Wm // 2) if big else Wm, **cfg)
+            res[name] = r = W.ternary(K, Wm, **cfg)
             log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s, {r['tflops']:.1f} TFLOP/s")
     for name, (T, off) in {"block_decode_8k_4b": (1, 8191), "block_verify_8_4b": (8, 8184),
                            "block_prefill_4k_4b": (4096, 0)}.items():
         if name in only:
             log(name)
-            big = T > 16
-            res[name] = r = W.block(max(2, K // 4) if big else K, max(1, Wm // 2) if big else Wm, T, off)
+            res[name] = r = W.block(K, Wm, T, off)
             log(f"  {r['ms'] * 1e3:.1f} us/step, {r['gbs']:.1f} GB/s, {r['tflops']:.1f} TFLOP/s")
     cpu = None
     if not args.no_cpu_baseline:
