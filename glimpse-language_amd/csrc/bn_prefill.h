@@ -18,7 +18,8 @@
 //   K/V tiles of 32 keys are copied HBM/L2 -> LDS by global_load_lds (no VGPRs). Rows p and p+16 of a tile
 //   share one 1 KB copy instruction; the pairs are padded (K: 16 B, V: 64 B per pair) so the K operand reads
 //   (16 rows x 16 B per 16 lanes) and the transposed V reads (4 rows x 64 B per 32 lanes) fall on distinct
-//   banks, and every LDS address is one per-lane base register plus an immediate.
+//   banks, and every LDS address is one per-lane base register plus an immediate. A wave's 8 copies of the next
+//   tile are issued one after each pair of the current tile's S^T MFMAs, not as a burst before them.
 //   S^T = K Q^T on v_mfma_f32_32x32x16_f16 (A = K from LDS, B = Q^T in registers; q comes as fp16 bits, an fp32
 //   q goes to prefill_hilo_kernel, which keeps its precision). Softmax in fp32, log2
 //   domain; the running max moves only when a row's max grows by more than 2^8, so O is rarely rescaled. The
@@ -143,32 +144,20 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     }
 
     // Tile copy (per group): wave w moves row pairs 4w .. 4w+3 of K and of V; lane l of an instruction loads
-    // row p + 16*(l/32), 16-byte chunk l%32, into LDS pair p at byte 16*l. The tile base is wave-uniform and
-    // the lane offset fixed; only a tile that reaches past the cache's last row clamps its rows (masked).
-    const uint32_t lane_go = (uint32_t)(16 * h * (int)kvd + r32 * 8) * 2u;
+    // row p + 16*(l/32), 16-byte chunk l%32, into LDS pair p at byte 16*l. The tile base is wave-uniform; rows past
+    // the cache's last row are clamped to it per lane (their scores are masked). No branch: the copies of the next
+    // tile sit in the same basic block as the current tile's S product, where they are interleaved with its MFMAs.
+    const uint32_t lane_go = (uint32_t)(r32 * 8) * 2u;
     auto issue_tile = [&](int j, uint8_t* st) {
-        const int j0 = j * PF_BK;
-        if (j0 + PF_BK <= nk) {
-            const char* kt = reinterpret_cast<const char*>(kb + (int64_t)(j0 + 4 * w) * kvd);
-            const char* vt = reinterpret_cast<const char*>(vb + (int64_t)(j0 + 4 * w) * kvd);
+        const int j0 = j * PF_BK, lim = nk - 1 - j0;  // last valid row of this tile
+        const char* kt = reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd);
+        const char* vt = reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = 4 * w + i;
-                __builtin_amdgcn_global_load_lds(kt + i * kvd * 2 + lane_go, (pf_lds_void_t*)(st + p * PF_KP), 16, 0, 0);
-                __builtin_amdgcn_global_load_lds(vt + i * kvd * 2 + lane_go, (pf_lds_void_t*)(st + PF_KB + p * PF_VP), 16,
-                                                 0, 0);
-            }
-        } else {
-            const int lim = nk - 1 - j0;  // last valid row of this tile
-            const char* kt = reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd);
-            const char* vt = reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = 4 * w + i;
-                const uint32_t go = (uint32_t)(min(p + 16 * h, lim) * (int)kvd + r32 * 8) * 2u;
-                __builtin_amdgcn_global_load_lds(kt + go, (pf_lds_void_t*)(st + p * PF_KP), 16, 0, 0);
-                __builtin_amdgcn_global_load_lds(vt + go, (pf_lds_void_t*)(st + PF_KB + p * PF_VP), 16, 0, 0);
-            }
+        for (int i = 0; i < 4; i++) {
+            const int p = 4 * w + i;
+            const uint32_t go = (uint32_t)(min(p + 16 * h, lim) * (int)kvd) * 2u + lane_go;
+            __builtin_amdgcn_global_load_lds(kt + go, (pf_lds_void_t*)(st + p * PF_KP), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vt + go, (pf_lds_void_t*)(st + PF_KB + p * PF_VP), 16, 0, 0);
         }
     };
 
@@ -203,8 +192,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     // one tile: its K/V are in stage `cur`, the next tile is copied into `nxt` meanwhile
     auto tile_step = [&](int it, const uint8_t* cur, uint8_t* nxt) {
         const int j = j_begin + it;
-        if (j + 1 < j_end) issue_tile(j + 1, nxt);
         if (j < j_end) {
+            // the next tile (the last one repeats itself into the free stage: no branch around the copies)
+            issue_tile(min(j + 1, j_end - 1), nxt);
             const uint8_t* kl = cur + k_lane;
             const uint8_t* vl = cur + v_lane;
             const int j0 = j * PF_BK;
@@ -216,9 +206,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int ks = 0; ks < 16; ks++) {
                 s = mfma32(pf_lds_h8(kl + ks * 32), qb[ks], s);
-                // keep up to 6 operand reads ahead of the MFMA that uses them (LDS latency under load)
+                // two operand reads, their two MFMAs, then one of the next tile's 8 copies: each copy's issue
+                // (tens of cycles of this wave) overlaps MFMAs in flight instead of holding up the first ones
+                // (a burst of 8 copies before the S product: prefill_4k 161-171 against 154-160 us)
                 if ((ks & 1) == 1) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // 2 DS reads
                 if ((ks & 1) == 1) __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMAs
+                if ((ks & 1) == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 tile copy
             }
 
             // causal mask on tiles that cross the diagonal; register r holds key j0 + 8(r/4) + 4h + r%4
