@@ -94,6 +94,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = wave >> 2, w = wave & 3;  // wave-uniform
     const int h = lane >> 5, r32 = lane & 31;
     const int KV = a.KV, ntq = a.ntq;
+    // every argument word the block needs is requested at entry, in one round trip (left alone, the compiler
+    // fetches them in several dependent batches before the first copy goes out)
+    asm volatile("" ::"s"(a.q16), "s"(a.q_ts), "s"(a.q_hs), "s"(a.kc), "s"(a.vc), "s"(a.gate), "s"(a.g_ts),
+                 "s"(a.g_hs), "s"(a.out), "s"(a.o_ts), "s"(a.o_hs), "s"(a.signs), "s"(a.dyn), "s"(a.T), "s"(a.off));
 
     // block -> (kv head, q-tile): longest q-tiles (highest index) first
     int kh, qt;
@@ -123,23 +127,20 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     const uint16_t* vb = a.vc + (int64_t)kh * D;
     const int head = kh * 4 + w;
 
-    // Q rows of the block (4 heads x 32 tokens, fp16) are read with coalesced row loads and staged in the free
-    // second stage of each group (heads 0-1 in group 0's, heads 2-3 in group 1's), padded rows. Waves w and w+4
-    // share the head, so each row is read from memory once.
-    auto q_stage = [&](int hq) -> uint8_t* { return lds_s1 + (hq >> 1) * PF_STAGE + (hq & 1) * 32 * PF_QP; };
+    // Q rows of the block (4 heads x 32 tokens, fp16) are copied by global_load_lds into the free second stage of
+    // each group (heads 0-1 in group 0's, heads 2-3 in group 1's) in a K tile's layout: rows p and p+16 of a head in
+    // one 1 KB copy, pairs PF_KP apart, so the Q^T operand reads are the K operand reads' conflict-free pattern. Wave w
+    // copies pairs 8 (w % 2) .. +7 of head w / 2. No VGPRs and no wait before the first K/V tile's copies go out too.
+    auto q_stage = [&](int hq) -> uint8_t* { return lds_s1 + (hq >> 1) * PF_STAGE + (hq & 1) * 16 * PF_KP; };
     {
-        u4 x[8];
+        const int hq = wave >> 1;
+        const uint16_t* qh = a.q16 + (int64_t)(kh * 4 + hq) * a.q_hs + 8 * r32;
+        uint8_t* const qs = q_stage(hq);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int R = 16 * wave + 2 * i + h;  // block row: head R/32, token R%32
-            const int tl = min(t0 + (R & 31), a.T - 1);
-            x[i] = *reinterpret_cast<const u4*>(a.q16 + (int64_t)tl * a.q_ts + (int64_t)(kh * 4 + (R >> 5)) * a.q_hs +
-                                                 8 * r32);
-        }
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int R = 16 * wave + 2 * i + h;
-            *reinterpret_cast<u4*>(q_stage(R >> 5) + (R & 31) * PF_QP + 16 * r32) = x[i];
+            const int p = 8 * (wave & 1) + i;
+            const int tl = min(t0 + p + 16 * h, a.T - 1);
+            __builtin_amdgcn_global_load_lds(qh + (int64_t)tl * a.q_ts, (pf_lds_void_t*)(qs + p * PF_KP), 16, 0, 0);
         }
     }
 
@@ -179,16 +180,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     uint8_t* const st0 = lds_s0 + g * PF_STAGE;  // this group's stages
     uint8_t* const st1 = lds_s1 + g * PF_STAGE;
     if (j_begin < j_end) issue_tile(j_begin, st0);
-    __syncthreads();  // Q rows staged
+    pf_wait_vm0();
+    __syncthreads();  // Q rows and the first K/V tile landed
     // Q^T operand: lane l holds token t0 + l%32 (clamped), dims 16ks + 8h .. +7, fp16
     h8 qb[16];
     {
-        const uint8_t* qr = q_stage(w) + r32 * PF_QP + 16 * h;
+        const uint8_t* qr = q_stage(w) + (r32 & 15) * PF_KP + (r32 >> 4) * 512 + 16 * h;
 #pragma unroll
         for (int ks = 0; ks < 16; ks++) qb[ks] = pf_lds_h8(qr + 32 * ks);
     }
-    pf_wait_vm0();
-    __syncthreads();  // first K/V tile landed; every wave holds its Q (the staging stage is free again)
+    __syncthreads();  // every wave holds its Q (the staging stage takes the next tile's copies)
     // one tile: its K/V are in stage `cur`, the next tile is copied into `nxt` meanwhile
     auto tile_step = [&](int it, const uint8_t* cur, uint8_t* nxt) {
         const int j = j_begin + it;
