@@ -43,7 +43,7 @@ constexpr int PF_KB = 16 * PF_KP;         // K tile bytes
 constexpr int PF_VB = 16 * PF_VP;         // V tile bytes
 constexpr int PF_STAGE = PF_KB + PF_VB;   // one K + V stage (34,048 B)
 constexpr int PF_XSLOT = 16384;           // O exchange per wave at the end: 4 tiles of 32 x 32 fp32
-constexpr int PF_QP = 528;                // row pitch of the fp16 Q staging rows in LDS
+constexpr int PF_QP = 528;                // row pitch of prefill_pair_kernel's fp16 Q staging rows in LDS
 
 struct PrefillArgs {
     const float* q;          // element t*q_ts + h*q_hs + d (fp32: prefill_hilo_kernel) ...
