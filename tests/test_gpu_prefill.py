@@ -109,3 +109,25 @@ def test_prefill_kernel_matches_default_path(pf, gpu, q16):
                         v_new=d["v_new"], gate=d["gate"], kind=ba.KIND_PREFILL)
     torch.cuda.synchronize()
     assert np.max(np.abs(out1.cpu().numpy() - out2)) < 1e-3
+
+
+@pytest.mark.parametrize("q16", [True, False])
+def test_prefill_q_and_gate_in_place_from_qproj(pf, q16):
+    """q read in place from the first half of a [T][H][512] q_proj-shaped buffer (q_ts = 512 H, q_hs = 512 elements)
+    and the gate from its second half, the layout the runtime's q projection writes: the strided Q copies into LDS
+    (fp16 q) and loads (fp32 q) give the packed layout's outputs bit for bit."""
+    torch, ctx, ws = pf
+    T, off, H, KV = 100, 37, 8, 2
+    inp = workload.layer(6400, T=T, off=off, H=H, KV=KV)
+    if q16:
+        fp16_exact(inp)
+    print(f"prefill q and gate in place: T={T} off={off} fp16 q {q16}", flush=True)
+    packed, d = run_case(pf, inp, q16=q16)
+    qp = torch.zeros((T, H, 512), dtype=torch.float32, device="cuda")
+    qp[:, :, :256] = d["q"]
+    qp[:, :, 256:] = d["gate"]
+    qsrc = qp.half() if q16 else qp
+    out = ba.attention(ctx, ws, qsrc[:, :, :256], d["kc"], d["vc"], off, gate=qp[:, :, 256:],
+                       q_strides=(512 * H, 512), g_strides=(512 * H, 512), kind=ba.KIND_PREFILL)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), packed), "strided q / gate differ from the packed layout"
