@@ -1204,12 +1204,28 @@ bn_status bn_kv_copy(bn_ctx* ctx, bn_stream stream, const bn_kv_state* from, con
         return set_err(ctx->err, BN_EINVAL, "states of different shapes");
     if (from->len > to->cap) return set_err(ctx->err, BN_EINVAL, "len %u exceeds the target's cap %u", from->len, to->cap);
     if (from->len == 0) return BN_OK;
-    const size_t w = kv_rows_bytes(from, from->len);
-    const size_t sp = kv_rows_bytes(from, from->cap), dp = kv_rows_bytes(to, to->cap);
-    hipError_t e = hipMemcpy2DAsync(to->kc, dp, from->kc, sp, w, from->n_layers, hipMemcpyDeviceToDevice, (hipStream_t)stream);
-    if (e == hipSuccess)
-        e = hipMemcpy2DAsync(to->vc, dp, from->vc, sp, w, from->n_layers, hipMemcpyDeviceToDevice, (hipStream_t)stream);
-    return hip_err(ctx, e, "KV copy");
+    if (!aligned16(from->kc) || !aligned16(from->vc) || !aligned16(to->kc) || !aligned16(to->vc)) {
+        // caches not 16-byte aligned: the runtime's 2-D copies
+        const size_t w = kv_rows_bytes(from, from->len);
+        const size_t sp = kv_rows_bytes(from, from->cap), dp = kv_rows_bytes(to, to->cap);
+        hipError_t e = hipMemcpy2DAsync(to->kc, dp, from->kc, sp, w, from->n_layers, hipMemcpyDeviceToDevice,
+                                        (hipStream_t)stream);
+        if (e == hipSuccess)
+            e = hipMemcpy2DAsync(to->vc, dp, from->vc, sp, w, from->n_layers, hipMemcpyDeviceToDevice,
+                                 (hipStream_t)stream);
+        return hip_err(ctx, e, "KV copy");
+    }
+    // rows are KV * 512 bytes, so a layer's used rows and the layer pitches are whole 16-byte groups
+    const int64_t w16 = (int64_t)(kv_rows_bytes(from, from->len) / 16);
+    const int64_t sp16 = (int64_t)(kv_rows_bytes(from, from->cap) / 16), dp16 = (int64_t)(kv_rows_bytes(to, to->cap) / 16);
+    const int64_t cpl = ceil_div(w16, 256 * bn::KVC_U), chunks = 2 * (int64_t)from->n_layers * cpl;
+    // the dispatch counts work-items in 32 bits: at most 2^24 - 1 blocks of 256 (a 256 GiB copy)
+    if (chunks > (int64_t)(UINT32_MAX / 256)) return set_err(ctx->err, BN_EINVAL, "KV copy too large for one launch");
+    bn_launch(ctx, bn::kv_copy_kernel, dim3((unsigned)chunks), dim3(256), 0,
+              (hipStream_t)stream, reinterpret_cast<const bn::u4*>(from->kc), reinterpret_cast<const bn::u4*>(from->vc),
+              reinterpret_cast<bn::u4*>(to->kc), reinterpret_cast<bn::u4*>(to->vc), w16, sp16, dp16,
+              (int)from->n_layers, (int)cpl);
+    return launched(ctx, "kv_copy_kernel");
 }
 
 size_t bn_kv_section_size(const bn_kv_state* s) {

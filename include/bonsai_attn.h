@@ -313,7 +313,8 @@ bn_status bn_attn_decode_ragged_noalloc(bn_ctx* ctx, bn_stream stream, const bn_
 
 /* ---- prefix-state snapshots -------------------------------------------------------------------------- */
 /* encode_copy_state's KV part: rows [0, from->len) of every layer from `from` into `to` (same n_layers and KV,
- * to->cap >= from->len); one 2-D device copy on `stream`. to->len is the caller's to set. */
+ * to->cap >= from->len); one kernel on `stream` for both caches (two 2-D device copies when a cache pointer is not
+ * 16-byte aligned). The caches must not overlap. to->len is the caller's to set. */
 bn_status bn_kv_copy(bn_ctx* ctx, bn_stream stream, const bn_kv_state* from, const bn_kv_state* to);
 /* Bytes of s's KV section (header + 2 * n_layers * len * KV * 256 * 2); 0 for a bad state. */
 size_t bn_kv_section_size(const bn_kv_state* s);

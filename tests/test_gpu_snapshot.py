@@ -77,6 +77,31 @@ def test_copy_between_states(gpu):
         ba.kv_copy(ctx, ba.kv_state(d_kc, d_vc, 301), ba.kv_state(d_kc4, d_vc4, 0))
 
 
+@pytest.mark.parametrize("n_layers,KV,cap_from,cap_to,length,shift", [
+    (40, 1, 70, 33, 3, 0),        # 96 16-byte groups per layer: one partial chunk; 80 layer-caches in one grid
+    (3, 4, 600, 520, 513, 0),     # 65,664 groups per layer: 64 whole chunks and a ragged 65th
+    (2, 2, 300, 256, 256, 0),     # exactly 16 chunks per layer, target sized to the prefix
+    (3, 2, 90, 80, 77, 4),        # caches 8 bytes off 16-byte alignment: the runtime's 2-D copies
+])
+def test_copy_ragged_and_unaligned(gpu, n_layers, KV, cap_from, cap_to, length, shift):
+    torch, ctx, _ = gpu
+    kc, vc = make_caches(0xE180 + length, n_layers, cap_from, KV, length)
+
+    def placed(x):  # x on the device at `shift` int16 elements past an allocation's start
+        flat = torch.zeros(x.size + shift, dtype=torch.int16, device="cuda")
+        flat[shift:] = torch.from_numpy(np.ascontiguousarray(x).reshape(-1).view(np.int16)).cuda()
+        return flat[shift:].view(x.shape)
+
+    d_kc, d_vc = placed(kc), placed(vc)
+    sentinel = np.full((n_layers, cap_to, KV, D), 0xFFFF, np.uint16)
+    t_kc, t_vc = placed(sentinel), placed(sentinel)
+    ba.kv_copy(ctx, ba.kv_state(d_kc, d_vc, length), ba.kv_state(t_kc, t_vc, 0))
+    torch.cuda.synchronize()
+    got_k, got_v = host16(t_kc), host16(t_vc)
+    assert np.array_equal(got_k[:, :length], kc[:, :length]) and np.array_equal(got_v[:, :length], vc[:, :length])
+    assert np.all(got_k[:, length:] == 0xFFFF) and np.all(got_v[:, length:] == 0xFFFF)
+
+
 def test_attention_over_restored_cache_is_identical(gpu):
     torch, ctx, ws = gpu
     inp = workload.layer(0xE200, T=1, off=999, H=8, KV=2)  # cache rows 0..999 hold the prefix, row 999 is new
