@@ -37,7 +37,9 @@ constexpr int PH_OP = 1040;             // row pitch (bytes) of a wave's output 
 // has the SIMD's whole register file (amdgpu_waves_per_eu 1): O (128), Q^T hi and lo (64 each), two S^T tiles and
 // the operand reads in flight. The K/V tiles go through a ring of 4 stages (tile j in stage
 // j % 4, copied three tiles ahead); one barrier per tile says that tile j + 1 has landed and that every wave has
-// left tile j - 1, whose stage the copy of tile j + 3 then reuses. Per tile the wave computes S^T(j + 1) = K(j + 1)
+// left tile j - 1, whose stage the copy of tile j + 3 then reuses. Tile j + 3's 8 copies go out one after every
+// second k-step of S^T(j + 1) (a burst of them after the barrier left the SIMD without MFMAs for their issue time:
+// 4-5% slower). Per tile the wave computes S^T(j + 1) = K(j + 1)
 // Q^T on the MFMA units while the VALU turns S^T(j) into P(j) (one k-step of each at a time), then O += P(j) V(j),
 // the operand reads a few MFMAs ahead of their use.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_hilo_kernel(PrefillArgs a) {
@@ -102,38 +104,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         asm volatile("" : "+v"(ql[ks]));
     }
 
-    // Tile copy into stage j % 4: wave w moves row pairs 4w .. 4w+3 of K and of V (8 copies); lane l of a copy loads
-    // row p + 16 (l / 32), 16-byte chunk l % 32, into LDS pair p at byte 16 l. Only a tile that reaches past the
-    // cache's last row clamps its rows (masked).
-    const uint32_t lane_go = (uint32_t)(16 * h * (int)kvd + r32 * 8) * 2u;
-    auto issue_tile = [&](int j) {
-        uint8_t* st = lds + (j & (PH_STAGES - 1)) * PF_STAGE;
-        const int j0 = j * PF_BK;
-        if (j0 + PF_BK <= nk) {
-            const char* kt = reinterpret_cast<const char*>(kb + (int64_t)(j0 + 4 * w) * kvd);
-            const char* vt = reinterpret_cast<const char*>(vb + (int64_t)(j0 + 4 * w) * kvd);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = 4 * w + i;
-                pf_copy16(kt + i * kvd * 2 + lane_go, st + p * PF_KP);
-                pf_copy16(vt + i * kvd * 2 + lane_go, st + PF_KB + p * PF_VP);
-            }
-        } else {
-            const int lim = nk - 1 - j0;  // last valid row of this tile
-            const char* kt = reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd);
-            const char* vt = reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = 4 * w + i;
-                const uint32_t go = (uint32_t)(min(p + 16 * h, lim) * (int)kvd + r32 * 8) * 2u;
-                pf_copy16(kt + go, st + p * PF_KP);
-                pf_copy16(vt + go, st + PF_KB + p * PF_VP);
-            }
-        }
+    // Tile copies: wave w moves row pairs 4w .. 4w+3 of K and of V (8 copies per tile); copy c of tile jt: K (c even)
+    // or V (c odd) of row pair 4 w + c / 2, lane l loading row 32 jt + p + 16 (l / 32), clamped to the cache's last row
+    // (those keys are masked), 16-byte chunk l % 32, into LDS pair p at byte 16 l.
+    auto tile_copy = [&](int jt, uint8_t* st, int c) __attribute__((always_inline)) {
+        const int j0 = jt * PF_BK, lim = nk - 1 - j0, p = 4 * w + (c >> 1);
+        const uint32_t go = (uint32_t)(min(p + 16 * h, lim) * (int)kvd + r32 * 8) * 2u;
+        if (c & 1)
+            pf_copy16(reinterpret_cast<const char*>(vb + (int64_t)j0 * kvd) + go, st + PF_KB + p * PF_VP);
+        else
+            pf_copy16(reinterpret_cast<const char*>(kb + (int64_t)j0 * kvd) + go, st + p * PF_KP);
     };
+    // tiles 0, 1, 2 into stages 0, 1, 2 (a tile past the last repeats the last: its stage is never read as such), so
+    // that every tile step finds the same copies in flight
 #pragma unroll
     for (int j = 0; j < PH_STAGES - 1; j++)
-        if (j < nt) issue_tile(j);
+#pragma unroll
+        for (int c = 0; c < 8; c++) tile_copy(min(j, nt - 1), lds + j * PF_STAGE, c);
 
     f16x o[8];
 #pragma unroll
@@ -149,12 +136,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     float* bc = reinterpret_cast<float*>(bc_lds[w]);
 
     // tile 0 landed (tiles 1 and 2 may still be in flight), for every wave; then S^T(0)
-    if (nt >= 3)
-        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-    else if (nt == 2)
-        asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-    else
-        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
     f16x s_cur;
     {
         const uint8_t* kl = lds + k_lane;
@@ -171,12 +153,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // Tile j: S^T(j + 1) from stage j + 1 (computed also after the last tile, from a stage whose copies are done,
     // and dropped), P(j) from S^T(j), O += P(j) V(j) from stage j.
     for (int j = 0; j < nt; j++) {
-        // tile j + 1 landed, and every wave is done with tile j - 1, whose stage takes tile j + 3
-        if (j + 2 < nt)
-            asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-        if (j + 3 < nt) issue_tile(j + 3);
+        // tile j + 1 landed (tile j + 2's copies may be in flight), and every wave is done with tile j - 1, whose
+        // stage takes tile j + 3 (a repeat of the last tile past the end), copied during the S^T(j + 1) MFMAs below
+        asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+        const int jc = min(j + 3, nt - 1);
+        uint8_t* cst = lds + ((j + 3) & (PH_STAGES - 1)) * PF_STAGE;
         const uint8_t* cur = lds + (j & (PH_STAGES - 1)) * PF_STAGE;
         const uint8_t* nxt = lds + ((j + 1) & (PH_STAGES - 1)) * PF_STAGE;
 
@@ -255,6 +236,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             else if (ks + VA >= 16) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             __builtin_amdgcn_sched_group_barrier(0x402, 4, 0);
+            if (ks & 1) {  // one copy after every second k-step's MFMAs, which stay ahead of it
+                tile_copy(jc, cst, ks >> 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
@@ -284,7 +269,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     f4 lv[4];
 #pragma unroll
     for (int gg = 0; gg < 4; gg++) lv[gg] = bc_lds[w][2 * gg + h];
-    __syncthreads();  // every wave is done with the stages (and every copy has landed: the last tiles waited for all)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last tile steps' copies (repeats) have landed
+    __syncthreads();  // every wave is done with the stages
     uint8_t* orow = lds + w * 32 * PH_OP;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++)
