@@ -291,7 +291,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
                 for (int e = 0; e < 4; e++) y[e] = gate_mul_fast(y[e], z[e]);
             }
-            *reinterpret_cast<f4*>(a.out + (int64_t)t * a.o_ts + (int64_t)head * a.o_hs + 4 * lane) = y;
+            __builtin_nontemporal_store(y, reinterpret_cast<f4*>(a.out + (int64_t)t * a.o_ts + (int64_t)head * a.o_hs +
+                                                               4 * lane));  // streamed out, as in prefill_kernel
         }
         return;
     }
@@ -318,8 +319,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         float* o_ = a.out + (int64_t)t * a.o_ts + (int64_t)(kh * 4 + 2 * p) * a.o_hs;
 #pragma unroll
         for (int i = 0; i < 2; i++)
-            *reinterpret_cast<f4*>(o_ + i * a.o_hs + 4 * lane) =
-                f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512;
+            __builtin_nontemporal_store(f4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]} * INV_SQRT512,
+                                        reinterpret_cast<f4*>(o_ + i * a.o_hs + 4 * lane));
     }
 }
 
