@@ -400,7 +400,10 @@ bn_status launch_decode(bn_ctx* ctx, hipStream_t st, const bn::DecodeArgs& d, co
     switch (p.waves) {
         case 1: bn_launch(ctx, bn::decode_split_kernel<1>, grid, dim3(64), 0, st, d); break;
         case 2:
-            if (p.xcd_rows)
+            // cached K/V loads where rows are shared (xcd_rows) or the launch holds at most one block per CU
+            // (latency-bound: single-sequence decodes over 32K keys 0.3-1 us faster, the rest unchanged); the wide
+            // streaming launches keep non-temporal loads (32 x 8K keys: 173-174 against 190-194 us cached)
+            if (p.xcd_rows || p.units * p.KV <= (int64_t)ctx->cus)
                 bn_launch(ctx, (bn::decode_split_kernel<2, true>), grid, dim3(128), 0, st, d);
             else
                 bn_launch(ctx, (bn::decode_split_kernel<2, false>), grid, dim3(128), 0, st, d);

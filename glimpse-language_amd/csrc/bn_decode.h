@@ -272,9 +272,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // W waves per block. A split's 16-key tiles are dealt to the waves in contiguous runs (wave w: tiles
 // [w nt / W, (w+1) nt / W)); each wave keeps its own online softmax, and the block merges the W partial
 // (m, l, acc) in wave order through LDS. One partial (or the finished output) per block.
-// SHARED: the K/V rows are read by several units (the rows of one sequence in the XCD-aware order): cached loads,
-// so the other rows find them in L2; otherwise non-temporal loads stream them (a compile-time choice: a branch in
-// the tile loop costs the streaming case 10%).
+// SHARED: cached K/V loads, for rows read by several units (the rows of one sequence in the XCD-aware order: the
+// other rows find them in L2) and for launches of at most one block per CU (latency-bound); otherwise non-temporal
+// loads stream them (a compile-time choice: a branch in the tile loop costs the streaming case 10%).
 template <int W, bool SHARED = false>
 __global__ __launch_bounds__(64 * W) void decode_split_kernel(DecodeArgs a) {
     __shared__ f4 p_lds[W][16];   // per wave: p[key in tile][head]
