@@ -678,10 +678,14 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
     asm volatile("" ::"s"(a.part), "s"(a.units), "s"(a.chunk), "s"(a.xcd_rows), "s"(a.gate), "s"(a.out), "s"(a.signs),
                  "s"(a.g_ss), "s"(a.g_hs), "s"(a.o_ss), "s"(a.o_hs), "s"(a.kv_len), "s"(a.dyn), "s"(a.len0),
                  "s"(a.target), "s"(a.max_splits), "s"(a.max_len), "s"(a.nseq));
+    const int h = 2 * j + i, head = kh * 4 + h;
+    // the gate of the wave that finishes this head goes out with the first loads (its address needs no length), so
+    // its round trip overlaps the length scan's and the records' instead of following them
+    f4 zg = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.gate && q == 0) zg = *reinterpret_cast<const f4*>(a.gate + seq * a.g_ss + head * a.g_hs + d0);
     const DecSplit sp = dec_find_seq(a, seq, lane);
     const int ns = sp.n;
     if (ns <= 1 && !a.chunk) return;  // written by the split kernel
-    const int h = 2 * j + i, head = kh * 4 + h;
     // the record of this wave's k-th split (split q + 4k)
     auto rec = [&](int k) -> const float* {
         return a.part + ((int64_t)kh * a.units + dec_slot(a, sp.P, seq, q + 4 * k)) * DEC_PART;
@@ -761,9 +765,8 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
         const float L = ((l_lds[wave] + l_lds[wave + 1]) + l_lds[wave + 2]) + l_lds[wave + 3];
         f4 y;
         if (a.gate) {
-            const f4 z = *reinterpret_cast<const f4*>(a.gate + seq * a.g_ss + head * a.g_hs + d0);
 #pragma unroll
-            for (int e = 0; e < 4; e++) y[e] = gate_mul(s[e] / L, z[e]);
+            for (int e = 0; e < 4; e++) y[e] = gate_mul(s[e] / L, zg[e]);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; e++) y[e] = s[e] / L;
